@@ -1,0 +1,271 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Workload (one "step"): the linear layers of one Qwen2.5-0.5B decode step at
+M=1, 4-bit group-64 affine weights with bf16 scales/biases:
+24 layers x {q 896->896, k 896->128, v 896->128, o 896->896, gate 896->4864,
+up 896->4864, down 4864->896} + lm_head 896->151936 = 169 quantized_matmul
+calls, 279,258,624 algorithmic bytes.  Weights are random (seeded, generated
+on the device); each projection has its own pre-generated x ~ N(0,1).  The
+169 launches of a step are captured once per weight replica into a HIP graph
+and replayed; three replicas (838 MB) rotate so consecutive steps never find
+their weights in the 256 MB Infinity Cache.
+
+Printed: one JSON line with the step throughput (value, GB/s), the roofline
+of the dominant kernel (the lm_head GEMV, 76.9 MB per launch), headline
+numbers (qmv 4096x14336 at M=1, qmm at M=2048) and the CPU baseline (the C
+oracle's fp32 path on the host cores, same step, one replica).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sen-mlx_amd"))
+
+METRIC = "qmv GB/s (% of HBM peak) at M=1; qmm TFLOP/s at M=2048, 4-bit g64"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+QWEN05_LAYER = [("q", 896, 896), ("k", 128, 896), ("v", 128, 896), ("o", 896, 896),
+                ("gate", 4864, 896), ("up", 4864, 896), ("down", 896, 4864)]
+QWEN05_LAYERS = 24
+LM_HEAD = ("lm_head", 151936, 896)
+
+
+def qbytes(M, N, K, bits=4, g=64, sb=2, xb=2, yb=2):
+    """algorithmic bytes: packed codes + scales + biases + x + y"""
+    return N * K * bits // 8 + 2 * N * (K // g) * sb + M * K * xb + M * N * yb
+
+
+def step_shapes():
+    shapes = []
+    for layer in range(QWEN05_LAYERS):
+        for name, N, K in QWEN05_LAYER:
+            shapes.append((f"l{layer}.{name}", N, K))
+    shapes.append(LM_HEAD)
+    return shapes
+
+
+class Proj:
+    __slots__ = ("name", "N", "K", "x", "w", "s", "b", "y")
+
+
+def make_replica(miqmm, torch, replica, shapes):
+    projs = []
+    for i, (name, N, K) in enumerate(shapes):
+        p = Proj()
+        p.name, p.N, p.K = name, N, K
+        p.x, p.w, p.s, p.b = miqmm.synth_problem(1, N, K, 64, 4, seed=replica, stream_id=i)
+        p.y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+        projs.append(p)
+    return projs
+
+
+def run_step(miqmm, projs):
+    for p in projs:
+        miqmm.quantized_matmul(p.x, p.w, p.s, p.b, True, 64, 4, out=p.y)
+
+
+def capture(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def time_graphs(torch, graphs, reps):
+    """events on the replay stream around `reps` replays; returns seconds"""
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(reps):
+        graphs[i % len(graphs)].replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3
+
+
+def kernel_roofline(miqmm, torch, N, K, M, replicas, launches_per_graph, reps):
+    """average duration of back-to-back launches of one shape over rotating
+    weight replicas (cold in the Infinity Cache); returns (avg_s, bytes_per_launch)"""
+    sets = []
+    for r in range(replicas):
+        x, w, s, b = miqmm.synth_problem(M, N, K, 64, 4, seed=100 + r, stream_id=N + K)
+        sets.append((x, w, s, b, torch.empty((M, N), dtype=torch.bfloat16, device="cuda")))
+
+    def body():
+        for i in range(launches_per_graph):
+            x, w, s, b, y = sets[i % replicas]
+            miqmm.quantized_matmul(x, w, s, b, True, 64, 4, out=y)
+
+    body()
+    torch.cuda.synchronize()
+    g = capture(torch, body)
+    g.replay()
+    t = time_graphs(torch, [g], reps)
+    del sets
+    return t / (reps * launches_per_graph), qbytes(M, N, K)
+
+
+def qmm_tflops(miqmm, torch, M, N, K, iters):
+    x, w, s, b = miqmm.synth_problem(M, N, K, 64, 4, seed=7, stream_id=N + K)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    for _ in range(2):
+        miqmm.quantized_matmul(x, w, s, b, True, 64, 4, out=y)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        miqmm.quantized_matmul(x, w, s, b, True, 64, 4, out=y)
+    end.record()
+    torch.cuda.synchronize()
+    t = start.elapsed_time(end) / 1e3 / iters
+    return 2.0 * M * N * K / t / 1e12, t
+
+
+def dense_bf16_tflops(torch, M, N, K, iters):
+    """hipBLASLt dense bf16 GEMM of the same shape (cross-check of the MFMA ceiling)"""
+    a = torch.randn((M, K), dtype=torch.bfloat16, device="cuda")
+    bt = torch.randn((N, K), dtype=torch.bfloat16, device="cuda")
+    for _ in range(2):
+        torch.matmul(a, bt.t())
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        torch.matmul(a, bt.t())
+    end.record()
+    torch.cuda.synchronize()
+    t = start.elapsed_time(end) / 1e3 / iters
+    return 2.0 * M * N * K / t / 1e12
+
+
+def cpu_baseline(miqmm, torch, projs, budget_s=12.0):
+    """the C oracle's fp32 path (OpenMP over N) on the host cores, on the same
+    decode step (one replica), repeated until ~budget_s of CPU time"""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    O.build_c_oracle()
+    threads = min(16, os.cpu_count() or 1)
+    host = []
+    for p in projs:
+        host.append((p.x.view(torch.int16).cpu().numpy().view(np.uint16),
+                     p.w.cpu().numpy().view(np.uint32),
+                     p.s.view(torch.int16).cpu().numpy().view(np.uint16),
+                     p.b.view(torch.int16).cpu().numpy().view(np.uint16), p.N, p.K))
+    step_bytes = sum(qbytes(1, N, K) for (_, _, _, _, N, K) in host)
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        for (x, w, s, b, N, K) in host:
+            O.c_qmm_f32(x, w, s, b, 1, N, K, 64, 4, nthreads=threads)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or steps >= 50:
+            break
+    return {"value": round(step_bytes * steps / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{steps} full decode steps (169 GEMVs, {step_bytes} B each) of one weight replica, "
+                      f"C oracle fp32 path (oracle/miqmm_oracle.c, gcc -O3 -fopenmp), {threads} threads, "
+                      f"{el:.1f} s; MLX's CPU backend is not available offline",
+            "ms_per_step": round(el / steps * 1e3, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--replicas", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-headline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the quantized-matmul path has no multi-GPU leg here "
+              "(sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import miqmm
+
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (torch.cuda.is_available() is False)", file=sys.stderr)
+        sys.exit(2)
+    miqmm.lib()
+    torch.cuda.set_device(0)
+
+    shapes = step_shapes()
+    step_bytes = sum(qbytes(1, N, K) for _, N, K in shapes)
+    replicas = [make_replica(miqmm, torch, r, shapes) for r in range(args.replicas)]
+    for projs in replicas:  # eager warm-up (loads the code objects before capture)
+        run_step(miqmm, projs)
+    torch.cuda.synchronize()
+    graphs = [capture(torch, (lambda p=projs: run_step(miqmm, p))) for projs in replicas]
+    time_graphs(torch, graphs, max(args.warmup, 1))
+    print(f"# timing {args.steps} decode steps ({len(shapes)} launches each)", file=sys.stderr, flush=True)
+    t = time_graphs(torch, graphs, args.steps)
+    gbs = step_bytes * args.steps / t / 1e9
+    ms_per_step = t / args.steps * 1e3
+
+    # dominant kernel of the step: the lm_head GEMV (N=151936, K=896)
+    lm_avg, lm_bytes = kernel_roofline(miqmm, torch, LM_HEAD[1], LM_HEAD[2], 1, replicas=8,
+                                       launches_per_graph=64, reps=8)
+    lm_gbs = lm_bytes / lm_avg / 1e9
+    out = {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "accumulate": "fp32",
+        "data": "synthetic (seeded on-device generator; random-init 4-bit g64 weights)",
+        "config": {"workload": "qwen2.5-0.5b decode step, linear layers only: 24 x {q 896->896, k 896->128, "
+                               "v 896->128, o 896->896, gate 896->4864, up 896->4864, down 4864->896} + "
+                               "lm_head 896->151936; M=1, 4-bit, group 64, bf16 x/scales/biases/y",
+                   "launches_per_step": len(shapes), "bytes_per_step": step_bytes,
+                   "weight_replicas": args.replicas, "hip_graph": True},
+        "roofline": {"kernel": "qmv lm_head 896->151936 M=1 (qmv_kernel<4,bf16,M1,RPS4>)", "bound": "hbm",
+                     "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_us": round(lm_avg * 1e6, 3), "bytes_per_launch": lm_bytes},
+    }
+    print(f"# step {ms_per_step * 1e3:.1f} us, {gbs:.1f} GB/s; lm_head {lm_avg * 1e6:.2f} us {lm_gbs:.1f} GB/s",
+          file=sys.stderr, flush=True)
+    del graphs, replicas
+    torch.cuda.empty_cache()
+
+    if not args.no_headline:
+        head = {}
+        avg, nb = kernel_roofline(miqmm, torch, 14336, 4096, 1, replicas=24, launches_per_graph=96, reps=6)
+        head["qmv_m1_4096x14336"] = {"us": round(avg * 1e6, 3), "GB/s": round(nb / avg / 1e9, 1),
+                                     "frac_hbm": round(nb / avg / 1e9 / HBM_PEAK_GBS, 4), "bytes": nb}
+        print(f"# qmv 4096x14336 M=1: {avg * 1e6:.2f} us {nb / avg / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+        for (N, K) in [(14336, 4096), (4096, 14336), (6144, 4096), (4096, 4096)]:
+            tf, tsec = qmm_tflops(miqmm, torch, 2048, N, K, iters=10)
+            head[f"qmm_m2048_{K}to{N}"] = {"TFLOP/s": round(tf, 1), "us": round(tsec * 1e6, 1),
+                                           "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+            print(f"# qmm M=2048 {K}->{N}: {tf:.1f} TFLOP/s ({tsec * 1e6:.1f} us)", file=sys.stderr, flush=True)
+        head["dense_bf16_gemm_m2048_4096to14336_torch"] = {
+            "TFLOP/s": round(dense_bf16_tflops(torch, 2048, 14336, 4096, 10), 1)}
+        out["headline"] = head
+        torch.cuda.empty_cache()
+
+    if not args.no_cpu_baseline:
+        projs = make_replica(miqmm, torch, 0, shapes)
+        out["cpu_baseline"] = cpu_baseline(miqmm, torch, projs)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,131 @@
+/*
+ * miqmm.h -- C ABI of the MI355X (gfx950) affine group-quantized matmul.
+ *
+ * Drop-in for the quantized-projection hot path of SenClaw/sen-mlx, which
+ * calls MLX's
+ *     quantized_matmul(x, w, scales, biases, transpose=true, group_size, bits)
+ * through mlx-rs (call shape: src/engine/mlx_lm/utils/mod.rs:70-78,
+ * src/engine/mlx_lm/models/bonsai_q1.rs:469-477) on every QuantizedLinear
+ * projection (src/engine/mlx_lm/models/llama.rs:195-197,249,293-294) and tied
+ * lm_head (llama.rs:511-517).  mlx-rs binds it to mlx-c's C function of the
+ * same name, whose conventions (int status, 0 = ok; caller-owned result;
+ * borrowed inputs; explicit stream) are those shown for the sibling op at
+ * src/engine/mlx_lm/utils/moe.rs:50-76.  This header keeps those conventions
+ * with plain device pointers instead of mlx_array handles.
+ *
+ * Layout (MLX affine quantization, transpose=true):
+ *   x       [M, K]            activation, row-major, dtype x_dtype (bf16)
+ *   w       [N, K*bits/32]    uint32 words; code k of row n is bits
+ *                             bits*(k mod 32/bits) .. of word k/(32/bits), LSB first
+ *   scales  [N, K/group_size] dtype sb_dtype (bf16 or fp16)
+ *   biases  [N, K/group_size] dtype sb_dtype
+ *   y       [M, N]            dtype y_dtype (bf16, fp16 or fp32)
+ *   y[m,n] = sum_k x[m,k] * (scales[n,k/g] * q[n,k] + biases[n,k/g])
+ *
+ * All pointers are device pointers owned by the caller; nothing is allocated
+ * on the matmul path.  Calls are asynchronous on `stream` (a hipStream_t;
+ * NULL = the default stream).  Every function returns a miqmm_status; on
+ * failure miqmm_last_error() returns a message for the calling thread.
+ * Calls are safe from several threads on distinct streams.
+ */
+#ifndef MIQMM_H
+#define MIQMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    MIQMM_OK = 0,
+    MIQMM_EINVAL = 1,  /* bad shape, pointer, alignment or argument value */
+    MIQMM_ENOTSUP = 2, /* valid for MLX but not provided here (e.g. transpose=false, bits=2) */
+    MIQMM_EHIP = 3     /* a HIP runtime error; miqmm_last_error() names it */
+} miqmm_status;
+
+typedef enum { MIQMM_DT_BF16 = 0, MIQMM_DT_F16 = 1, MIQMM_DT_F32 = 2 } miqmm_dtype;
+
+typedef enum { MIQMM_ROUTE_AUTO = 0, MIQMM_ROUTE_QMV = 1, MIQMM_ROUTE_QMM = 2 } miqmm_route;
+
+/*
+ * y = quantized_matmul(x, w, scales, biases, transpose, group_size, bits).
+ * Replaces mlx_rs::ops::quantized_matmul / mlx-c mlx_quantized_matmul
+ * (reached at src/engine/mlx_lm/utils/mod.rs:70-78 and from every
+ * QuantizedLinear::forward).  transpose must be 1; bits in {4, 8};
+ * group_size in {32, 64, 128}; K % group_size == 0; x and w 16-byte aligned.
+ * M == 0 is a no-op.  Route: M <= 16 -> qmv (HBM-bound GEMV), else qmm (MFMA).
+ */
+int miqmm_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
+                           const void* biases, int64_t M, int64_t N, int64_t K, int transpose,
+                           int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
+                           void* stream);
+
+/*
+ * As miqmm_quantized_matmul, with the route forced (MIQMM_ROUTE_QMV accepts
+ * any M, one pass over W per 16 rows of x; MIQMM_ROUTE_QMM any M >= 1).
+ * Used by tests to hold both routes to the same oracle on one shape.
+ */
+int miqmm_quantized_matmul_ex(void* y, const void* x, const uint32_t* w, const void* scales,
+                              const void* biases, int64_t M, int64_t N, int64_t K, int transpose,
+                              int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
+                              int route, void* stream);
+
+/*
+ * QuantizedLinear forward: y = quantized_matmul(...) rounded to y_dtype, then
+ * + bias[n] rounded again (bias may be NULL; dtype y_dtype), i.e. the two ops
+ * of MaybeQuantized<Linear>::forward for a quantized slot with a bias
+ * (src/engine/mlx_lm/models/llama.rs:94-98,139-147 q/k/v bias of Qwen2).
+ */
+int miqmm_quantized_linear(void* y, const void* x, const uint32_t* w, const void* scales,
+                           const void* biases, const void* bias, int64_t M, int64_t N, int64_t K,
+                           int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
+                           void* stream);
+
+/*
+ * out[n, k] = scales[n,k/g] * q[n,k] + biases[n,k/g] (fp32 fma, stored as
+ * out_dtype).  Replaces mlx_rs::ops::dequantize as used beside the
+ * reference's quantized-matmul test (src/engine/mlx_lm/utils/moe.rs:118-126).
+ */
+int miqmm_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
+                     int64_t N, int64_t K, int group_size, int bits, int sb_dtype, int out_dtype,
+                     void* stream);
+
+/*
+ * codes[n*K + k] = q[n, k] (uint8): the kernels' unpacking convention,
+ * exposed so it can be checked bit-exactly against the packed layout of
+ * src/engine/mlx_lm/models/bonsai_q1.rs:137-143 (bits=1), generalised.
+ */
+int miqmm_unpack(uint8_t* codes, const uint32_t* w, int64_t N, int64_t K, int bits, void* stream);
+
+/*
+ * Which route and tiling miqmm_quantized_matmul picks for a shape (host
+ * only, no GPU access).  route_out: MIQMM_ROUTE_QMV / _QMM.  tile_out[4]:
+ * qmv -> {rows per wave, M tile, 0, 0}; qmm -> {BM, BN, BK, 0}.
+ * No reference counterpart: reporting for benches and tests.
+ */
+int miqmm_query_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, int* route_out,
+                      int* tile_out);
+
+/*
+ * Seeded synthetic problem on the device, bit-identical to the oracle's
+ * generator: x ~ N(0,1) (Irwin-Hall(4)), codes uniform in [0, 2^bits),
+ * scales = |N(0,1)|*0.02, biases = -2^(bits-1)*scale + N(0,1)*0.002.  Any
+ * of x, w, scales/biases may be NULL to skip it.  No reference counterpart:
+ * input generation for benches and tests.
+ */
+int miqmm_synth_problem(void* x, uint32_t* w, void* scales, void* biases, int64_t M, int64_t N,
+                        int64_t K, int group_size, int bits, int x_dtype, int sb_dtype,
+                        uint64_t seed, uint64_t stream_id, void* stream);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* miqmm_last_error(void);
+
+/* Library version string. */
+const char* miqmm_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIQMM_H */

@@ -1,0 +1,190 @@
+// api.cpp -- the C ABI (include/miqmm.h): argument validation on the host,
+// route choice and launch.  Validation mirrors the checks MLX performs before
+// recording a quantized_matmul node, returning a status the way mlx-c does
+// (src/engine/mlx_lm/utils/moe.rs:66-76: nonzero status, message on the side).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/miqmm.h"
+#include "miqmm_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return MIQMM_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int64_t kMaxDim = (int64_t)1 << 31;
+
+int check_quant(int64_t N, int64_t K, int group_size, int bits, int sb_dtype) {
+    if (bits != 4 && bits != 8) {
+        if (bits == 2 || bits == 3 || bits == 5 || bits == 6)
+            return fail(MIQMM_ENOTSUP, "bits=%d is a valid MLX width but only 4 and 8 are provided", bits);
+        return fail(MIQMM_EINVAL, "bits must be 4 or 8, got %d", bits);
+    }
+    if (group_size != 32 && group_size != 64 && group_size != 128)
+        return fail(MIQMM_EINVAL, "group_size must be 32, 64 or 128, got %d", group_size);
+    if (N <= 0 || K <= 0 || N >= kMaxDim || K >= kMaxDim)
+        return fail(MIQMM_EINVAL, "N and K must be in [1, 2^31), got N=%lld K=%lld", (long long)N, (long long)K);
+    if (K % group_size != 0)
+        return fail(MIQMM_EINVAL, "K=%lld is not a multiple of group_size=%d", (long long)K, group_size);
+    if (sb_dtype != MIQMM_DT_BF16 && sb_dtype != MIQMM_DT_F16)
+        return fail(MIQMM_ENOTSUP, "scales/biases dtype %d not supported (bf16=0, f16=1)", sb_dtype);
+    return MIQMM_OK;
+}
+
+int check_launch(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(MIQMM_EHIP, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+               const void* bias, int64_t M, int64_t N, int64_t K, int transpose, int group_size,
+               int bits, int x_dtype, int sb_dtype, int y_dtype, int route, void* stream) {
+    if (!transpose)
+        return fail(MIQMM_ENOTSUP, "transpose=false is not provided (every live call site uses transpose=true)");
+    int st = check_quant(N, K, group_size, bits, sb_dtype);
+    if (st != MIQMM_OK) return st;
+    if (M < 0 || M >= kMaxDim) return fail(MIQMM_EINVAL, "M must be in [0, 2^31), got %lld", (long long)M);
+    if (x_dtype != MIQMM_DT_BF16) return fail(MIQMM_ENOTSUP, "x dtype %d not supported (bf16=0)", x_dtype);
+    if (y_dtype != MIQMM_DT_BF16 && y_dtype != MIQMM_DT_F16 && y_dtype != MIQMM_DT_F32)
+        return fail(MIQMM_EINVAL, "y dtype %d invalid", y_dtype);
+    if (route != MIQMM_ROUTE_AUTO && route != MIQMM_ROUTE_QMV && route != MIQMM_ROUTE_QMM)
+        return fail(MIQMM_EINVAL, "route %d invalid", route);
+    if (M == 0) return ok();
+    if (!y || !x || !w || !scales || !biases) return fail(MIQMM_EINVAL, "null pointer argument");
+    if (!aligned16(x) || !aligned16(w))
+        return fail(MIQMM_EINVAL, "x and w must be 16-byte aligned");
+    if (M * K >= ((int64_t)1 << 40) || M * N >= ((int64_t)1 << 40))
+        return fail(MIQMM_EINVAL, "M*K or M*N too large");
+
+    miqmm::QmmArgs a{y, x, w, scales, biases, bias, M, N, K, group_size, bits, x_dtype, sb_dtype, y_dtype,
+                     reinterpret_cast<hipStream_t>(stream)};
+    if (route == MIQMM_ROUTE_AUTO) route = M <= 16 ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
+    if (route == MIQMM_ROUTE_QMV) {
+        // the qmv kernel handles at most 16 rows of x per pass over W
+        for (int64_t m0 = 0; m0 < M; m0 += 16) {
+            miqmm::QmmArgs part = a;
+            const int64_t mm = M - m0 < 16 ? M - m0 : 16;
+            part.M = mm;
+            part.x = static_cast<const uint16_t*>(x) + m0 * K;
+            const int ysz = y_dtype == MIQMM_DT_F32 ? 4 : 2;
+            part.y = static_cast<char*>(y) + m0 * N * ysz;
+            st = check_launch(miqmm::launch_qmv(part), "qmv launch");
+            if (st != MIQMM_OK) return st;
+        }
+        return ok();
+    }
+    return check_launch(miqmm::launch_qmm(a), "qmm launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int miqmm_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
+                           const void* biases, int64_t M, int64_t N, int64_t K, int transpose,
+                           int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
+                           void* stream) {
+    return qmm_common(y, x, w, scales, biases, nullptr, M, N, K, transpose, group_size, bits, x_dtype,
+                      sb_dtype, y_dtype, MIQMM_ROUTE_AUTO, stream);
+}
+
+int miqmm_quantized_matmul_ex(void* y, const void* x, const uint32_t* w, const void* scales,
+                              const void* biases, int64_t M, int64_t N, int64_t K, int transpose,
+                              int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
+                              int route, void* stream) {
+    return qmm_common(y, x, w, scales, biases, nullptr, M, N, K, transpose, group_size, bits, x_dtype,
+                      sb_dtype, y_dtype, route, stream);
+}
+
+int miqmm_quantized_linear(void* y, const void* x, const uint32_t* w, const void* scales,
+                           const void* biases, const void* bias, int64_t M, int64_t N, int64_t K,
+                           int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
+                           void* stream) {
+    return qmm_common(y, x, w, scales, biases, bias, M, N, K, 1, group_size, bits, x_dtype, sb_dtype,
+                      y_dtype, MIQMM_ROUTE_AUTO, stream);
+}
+
+int miqmm_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
+                     int64_t N, int64_t K, int group_size, int bits, int sb_dtype, int out_dtype,
+                     void* stream) {
+    int st = check_quant(N, K, group_size, bits, sb_dtype);
+    if (st != MIQMM_OK) return st;
+    if (out_dtype != MIQMM_DT_BF16 && out_dtype != MIQMM_DT_F16 && out_dtype != MIQMM_DT_F32)
+        return fail(MIQMM_EINVAL, "out dtype %d invalid", out_dtype);
+    if (!out || !w || !scales || !biases) return fail(MIQMM_EINVAL, "null pointer argument");
+    return check_launch(miqmm::launch_dequantize(out, w, scales, biases, N, K, group_size, bits, sb_dtype,
+                                                 out_dtype, reinterpret_cast<hipStream_t>(stream)),
+                        "dequantize launch");
+}
+
+int miqmm_unpack(uint8_t* codes, const uint32_t* w, int64_t N, int64_t K, int bits, void* stream) {
+    if (bits != 4 && bits != 8) return fail(MIQMM_EINVAL, "bits must be 4 or 8, got %d", bits);
+    if (N <= 0 || K <= 0 || K % 32 != 0) return fail(MIQMM_EINVAL, "need N > 0 and K > 0 with K %% 32 == 0");
+    if (!codes || !w) return fail(MIQMM_EINVAL, "null pointer argument");
+    return check_launch(miqmm::launch_unpack(codes, w, N, K, bits, reinterpret_cast<hipStream_t>(stream)),
+                        "unpack launch");
+}
+
+int miqmm_query_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, int* route_out,
+                      int* tile_out) {
+    int st = check_quant(N, K, group_size, bits, MIQMM_DT_BF16);
+    if (st != MIQMM_OK) return st;
+    if (M < 0) return fail(MIQMM_EINVAL, "M must be >= 0");
+    miqmm::QmmArgs a{};
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.group_size = group_size;
+    a.bits = bits;
+    const int route = M <= 16 ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
+    if (route_out) *route_out = route;
+    if (tile_out) {
+        tile_out[0] = tile_out[1] = tile_out[2] = tile_out[3] = 0;
+        if (route == MIQMM_ROUTE_QMV) miqmm::qmv_config(a, &tile_out[0], &tile_out[1]);
+        else miqmm::qmm_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
+    }
+    return ok();
+}
+
+int miqmm_synth_problem(void* x, uint32_t* w, void* scales, void* biases, int64_t M, int64_t N,
+                        int64_t K, int group_size, int bits, int x_dtype, int sb_dtype,
+                        uint64_t seed, uint64_t stream_id, void* stream) {
+    int st = check_quant(N, K, group_size, bits, sb_dtype);
+    if (st != MIQMM_OK) return st;
+    if (x_dtype != MIQMM_DT_BF16 && x_dtype != MIQMM_DT_F16)
+        return fail(MIQMM_EINVAL, "x dtype %d invalid", x_dtype);
+    if (M < 0) return fail(MIQMM_EINVAL, "M must be >= 0");
+    if ((scales == nullptr) != (biases == nullptr))
+        return fail(MIQMM_EINVAL, "scales and biases are generated together");
+    return check_launch(miqmm::launch_synth(x, w, scales, biases, M, N, K, group_size, bits, x_dtype, sb_dtype,
+                                            seed, stream_id, reinterpret_cast<hipStream_t>(stream)),
+                        "synth launch");
+}
+
+const char* miqmm_last_error(void) { return g_last_error.c_str(); }
+
+const char* miqmm_version(void) { return "miqmm 0.1.0 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,182 @@
+// aux.hip -- dequantize / unpack kernels and the on-device synthetic-input
+// generator.
+//
+// dequantize: MLX's dequantize(w, scales, biases, group_size, bits) as the
+// reference uses it next to its only quantized-matmul test
+// (src/engine/mlx_lm/utils/moe.rs:118-126): out[n, k] = fma(s, q, b) in fp32
+// (src/engine/mlx_lm/models/bonsai_q1.rs:172), stored in the output dtype.
+//
+// synth: splitmix64 counter hash, draw i of stream (seed, tag) is
+// mix64(mix64(seed*G + tag) + i*G) with G = 0x9E3779B97F4A7C15; an
+// approximately N(0,1) value is the Irwin-Hall(4) sum of the draw's four
+// 16-bit fields, centred and scaled by one fp32 multiply.  Every float step
+// is one IEEE operation with contraction disabled, so host and device
+// generators produce identical bits.
+#include "miqmm_device.h"
+#include "miqmm_internal.h"
+
+namespace miqmm {
+namespace {
+
+constexpr uint64_t kGamma = 0x9E3779B97F4A7C15ull;
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__host__ __device__ __forceinline__ uint64_t stream_key_host(uint64_t seed, uint64_t tag) {
+    uint64_t z = seed * kGamma + tag;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float ih_normal(uint64_t r) {
+    const int32_t s = (int32_t)(r & 0xffffu) + (int32_t)((r >> 16) & 0xffffu) +
+                      (int32_t)((r >> 32) & 0xffffu) + (int32_t)((r >> 48) & 0xffffu);
+    return __fmul_rn((float)(s - 131070), 2.6428997e-05f);
+}
+
+template <int DT>
+__device__ __forceinline__ uint16_t to_half(float f) {
+    if constexpr (DT == DT_F16) return f32_to_f16_bits(f);
+    else return f32_to_bf16_bits(f);
+}
+
+template <int DT>
+__global__ void synth_normal_kernel(uint16_t* __restrict__ out, int64_t count, uint64_t key, float sigma) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    out[i] = to_half<DT>(__fmul_rn(ih_normal(mix64(key + (uint64_t)i * kGamma)), sigma));
+}
+
+__global__ void synth_codes_kernel(uint32_t* __restrict__ w, int64_t N, int64_t K, int bits, uint64_t key) {
+    const int per = 32 / bits;
+    const int64_t words = K / per;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * words) return;
+    const int64_t n = i / words, j = i % words;
+    uint32_t word = 0;
+    for (int t = 0; t < per; ++t) {
+        const uint64_t idx = (uint64_t)(n * K + j * per + t);
+        const uint32_t q = (uint32_t)(mix64(key + idx * kGamma) >> (64 - bits));
+        word |= q << (bits * t);
+    }
+    w[i] = word;
+}
+
+template <int DT>
+__global__ void synth_sb_kernel(uint16_t* __restrict__ s, uint16_t* __restrict__ b, int64_t count,
+                                int bits, uint64_t ks, uint64_t kb) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    const float sv = __fmul_rn(fabsf(ih_normal(mix64(ks + (uint64_t)i * kGamma))), 0.02f);
+    const uint16_t sh = to_half<DT>(sv);
+    const float sr = half_to_f32<DT>(sh);
+    const float noise = __fmul_rn(ih_normal(mix64(kb + (uint64_t)i * kGamma)), 0.002f);
+    const float bv = __fadd_rn(__fmul_rn(-(float)(1u << (bits - 1)), sr), noise);
+    s[i] = sh;
+    b[i] = to_half<DT>(bv);
+}
+
+template <int SBT>
+__global__ void dequantize_kernel(void* __restrict__ out, const uint32_t* __restrict__ w,
+                                  const uint16_t* __restrict__ sc, const uint16_t* __restrict__ bi,
+                                  int64_t N, int64_t K, int gs_shift, int bits, int out_dtype) {
+    const int per = 32 / bits;
+    const int64_t words = K / per;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * words) return;
+    const int64_t n = i / words, j = i % words;
+    const uint32_t word = w[i];
+    const uint32_t mask = (1u << bits) - 1u;
+    const int64_t G = K >> gs_shift;
+    for (int t = 0; t < per; ++t) {
+        const int64_t k = j * per + t;
+        const float s = half_to_f32<SBT>(sc[n * G + (k >> gs_shift)]);
+        const float b = half_to_f32<SBT>(bi[n * G + (k >> gs_shift)]);
+        const float v = fmaf(s, (float)((word >> (bits * t)) & mask), b);
+        const int64_t o = n * K + k;
+        if (out_dtype == DT_F32) ((float*)out)[o] = v;
+        else if (out_dtype == DT_F16) ((uint16_t*)out)[o] = f32_to_f16_bits(v);
+        else ((uint16_t*)out)[o] = f32_to_bf16_bits(v);
+    }
+}
+
+__global__ void unpack_kernel(uint8_t* __restrict__ codes, const uint32_t* __restrict__ w, int64_t N,
+                              int64_t K, int bits) {
+    const int per = 32 / bits;
+    const int64_t words = K / per;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * words) return;
+    const uint32_t word = w[i];
+    const uint32_t mask = (1u << bits) - 1u;
+    const int64_t n = i / words, j = i % words;
+    for (int t = 0; t < per; ++t) codes[n * K + j * per + t] = (uint8_t)((word >> (bits * t)) & mask);
+}
+
+inline unsigned blocks_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
+
+}  // namespace
+
+hipError_t launch_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
+                             int64_t N, int64_t K, int group_size, int bits, int sb_dtype,
+                             int out_dtype, hipStream_t stream) {
+    const int64_t total = N * (K * bits / 32);
+    const int gs_shift = __builtin_ctz((unsigned)group_size);
+    if (sb_dtype == DT_F16)
+        hipLaunchKernelGGL(dequantize_kernel<DT_F16>, dim3(blocks_for(total, 256)), dim3(256), 0, stream,
+                           out, w, (const uint16_t*)scales, (const uint16_t*)biases, N, K, gs_shift, bits, out_dtype);
+    else
+        hipLaunchKernelGGL(dequantize_kernel<DT_BF16>, dim3(blocks_for(total, 256)), dim3(256), 0, stream,
+                           out, w, (const uint16_t*)scales, (const uint16_t*)biases, N, K, gs_shift, bits, out_dtype);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpack(uint8_t* codes, const uint32_t* w, int64_t N, int64_t K, int bits, hipStream_t stream) {
+    const int64_t total = N * (K * bits / 32);
+    hipLaunchKernelGGL(unpack_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, stream, codes, w, N, K, bits);
+    return hipGetLastError();
+}
+
+hipError_t launch_synth(void* x, uint32_t* w, void* scales, void* biases, int64_t M, int64_t N,
+                        int64_t K, int group_size, int bits, int x_dtype, int sb_dtype,
+                        uint64_t seed, uint64_t stream_id, hipStream_t stream) {
+    const uint64_t tag = stream_id * 8u;
+    if (x && M > 0) {
+        const uint64_t key = stream_key_host(seed, tag + 1);
+        const int64_t count = M * K;
+        if (x_dtype == DT_F16)
+            hipLaunchKernelGGL(synth_normal_kernel<DT_F16>, dim3(blocks_for(count, 256)), dim3(256), 0, stream,
+                               (uint16_t*)x, count, key, 1.0f);
+        else
+            hipLaunchKernelGGL(synth_normal_kernel<DT_BF16>, dim3(blocks_for(count, 256)), dim3(256), 0, stream,
+                               (uint16_t*)x, count, key, 1.0f);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (w) {
+        const int64_t total = N * (K * bits / 32);
+        hipLaunchKernelGGL(synth_codes_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, stream, w, N, K,
+                           bits, stream_key_host(seed, tag + 2));
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (scales && biases) {
+        const int64_t count = N * (K / group_size);
+        const uint64_t ks = stream_key_host(seed, tag + 3), kb = stream_key_host(seed, tag + 4);
+        if (sb_dtype == DT_F16)
+            hipLaunchKernelGGL(synth_sb_kernel<DT_F16>, dim3(blocks_for(count, 256)), dim3(256), 0, stream,
+                               (uint16_t*)scales, (uint16_t*)biases, count, bits, ks, kb);
+        else
+            hipLaunchKernelGGL(synth_sb_kernel<DT_BF16>, dim3(blocks_for(count, 256)), dim3(256), 0, stream,
+                               (uint16_t*)scales, (uint16_t*)biases, count, bits, ks, kb);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace miqmm

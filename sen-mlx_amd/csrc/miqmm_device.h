@@ -1,0 +1,109 @@
+// miqmm_device.h -- gfx950 device helpers shared by the miqmm kernels.
+//
+// Packed affine layout (MLX, LSB-first; reference src/engine/mlx_lm/models/
+// bonsai_q1.rs:137-143 for bits=1, generalised): row n of W holds K*bits/32
+// uint32 words and code k sits in word k/(32/bits) at bit bits*(k mod 32/bits).
+// Dequant is w = scale*q + bias per group of `group_size` consecutive k
+// (bonsai_q1.rs:172).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace miqmm {
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+
+enum : int { DT_BF16 = 0, DT_F16 = 1, DT_F32 = 2 };
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <int DT>
+__device__ __forceinline__ float half_to_f32(uint16_t h) {
+    if constexpr (DT == DT_F16) return f16_bits_to_f32(h);
+    else return bf16_bits_to_f32(h);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);  // v_cvt_pk_bf16_f32, RNE
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, RNE
+}
+
+// store one output element in the requested dtype; `bias` (nullable, dtype of
+// y) is added after the matmul result is rounded, as QuantizedLinear does
+// (quantized_matmul, then + bias as a separate op).
+__device__ __forceinline__ void store_out(void* y, int64_t idx, int y_dtype, float v,
+                                          const void* bias, int64_t bidx) {
+    if (y_dtype == DT_F32) {
+        if (bias) v += ((const float*)bias)[bidx];
+        ((float*)y)[idx] = v;
+    } else if (y_dtype == DT_F16) {
+        uint16_t h = f32_to_f16_bits(v);
+        if (bias) h = f32_to_f16_bits(f16_bits_to_f32(h) + f16_bits_to_f32(((const uint16_t*)bias)[bidx]));
+        ((uint16_t*)y)[idx] = h;
+    } else {
+        uint16_t h = f32_to_bf16_bits(v);
+        if (bias) h = f32_to_bf16_bits(bf16_bits_to_f32(h) + bf16_bits_to_f32(((const uint16_t*)bias)[bidx]));
+        ((uint16_t*)y)[idx] = h;
+    }
+}
+
+// ---------------------------------------------------------------- bit tricks
+// bf16 with bits 0x4300|q is exactly 128+q for q < 128: a 4-bit code becomes
+// an exact bf16 operand with one and-or.  Pairs are (q_j, q_{j+4}) of a word.
+constexpr uint32_t kMagic128x2 = 0x43004300u;
+constexpr uint32_t kOnesBf16x2 = 0x3F803F80u;  // (1.0, 1.0)
+
+__device__ __forceinline__ bf16x2_t as_bf16x2(uint32_t u) { return __builtin_bit_cast(bf16x2_t, u); }
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a), as_bf16x2(b), c, false);
+}
+
+// word of eight 4-bit codes -> four bf16 pairs (q_j+128, q_{j+4}+128), j=0..3
+__device__ __forceinline__ void unpack4_magic(uint32_t w, uint32_t p[4]) {
+    p[0] = (w & 0x000F000Fu) | kMagic128x2;
+    p[1] = ((w >> 4) & 0x000F000Fu) | kMagic128x2;
+    p[2] = ((w >> 8) & 0x000F000Fu) | kMagic128x2;
+    p[3] = ((w >> 12) & 0x000F000Fu) | kMagic128x2;
+}
+
+// x words (x0|x1, x2|x3, x4|x5, x6|x7) -> pairs (x_j, x_{j+4}) matching unpack4_magic
+__device__ __forceinline__ void perm_x_for4(const uint32_t xw[4], uint32_t X[4]) {
+    X[0] = __builtin_amdgcn_perm(xw[2], xw[0], 0x05040100u);
+    X[1] = __builtin_amdgcn_perm(xw[2], xw[0], 0x07060302u);
+    X[2] = __builtin_amdgcn_perm(xw[3], xw[1], 0x05040100u);
+    X[3] = __builtin_amdgcn_perm(xw[3], xw[1], 0x07060302u);
+}
+
+// float value of byte I of w (selected as one v_cvt_f32_ubyteI)
+template <int I>
+__device__ __forceinline__ float ubyte_f32(uint32_t w) { return (float)((w >> (8 * I)) & 0xffu); }
+
+// word of four 8-bit codes -> two exact bf16 pairs (q0,q1), (q2,q3): the fp32
+// value of an integer <= 255 has zero low 16 bits, so its top half is exact.
+__device__ __forceinline__ void unpack8_pairs(uint32_t w, uint32_t p[2]) {
+    uint32_t f0 = __float_as_uint(ubyte_f32<0>(w));
+    uint32_t f1 = __float_as_uint(ubyte_f32<1>(w));
+    uint32_t f2 = __float_as_uint(ubyte_f32<2>(w));
+    uint32_t f3 = __float_as_uint(ubyte_f32<3>(w));
+    p[0] = __builtin_amdgcn_perm(f1, f0, 0x07060302u);
+    p[1] = __builtin_amdgcn_perm(f3, f2, 0x07060302u);
+}
+
+__device__ __forceinline__ u32x4_t ldg16(const void* p) {
+    return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+}  // namespace miqmm

@@ -1,0 +1,39 @@
+// miqmm_internal.h -- launcher declarations shared between the kernels and
+// the C ABI (api.cpp).  Host-side only types; no torch.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace miqmm {
+
+struct QmmArgs {
+    void* y;
+    const void* x;
+    const uint32_t* w;
+    const void* scales;
+    const void* biases;
+    const void* bias;  // optional [N] (QuantizedLinear), dtype of y
+    int64_t M, N, K;
+    int group_size, bits;
+    int x_dtype, sb_dtype, y_dtype;
+    hipStream_t stream;
+};
+
+// route launchers; return hipSuccess or the launch error
+hipError_t launch_qmv(const QmmArgs& a);
+hipError_t launch_qmm(const QmmArgs& a);
+
+// qmv tiling used for a given problem (rows per wave, M tile); for reporting
+void qmv_config(const QmmArgs& a, int* rows_per_wave, int* m_tile);
+void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk);
+
+hipError_t launch_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
+                             int64_t N, int64_t K, int group_size, int bits, int sb_dtype,
+                             int out_dtype, hipStream_t stream);
+hipError_t launch_unpack(uint8_t* codes, const uint32_t* w, int64_t N, int64_t K, int bits,
+                         hipStream_t stream);
+hipError_t launch_synth(void* x, uint32_t* w, void* scales, void* biases, int64_t M, int64_t N,
+                        int64_t K, int group_size, int bits, int x_dtype, int sb_dtype,
+                        uint64_t seed, uint64_t stream_id, hipStream_t stream);
+
+}  // namespace miqmm

@@ -1,0 +1,228 @@
+"""miqmm -- MI355X (gfx950) affine group-quantized matmul behind a C ABI.
+
+Host-side mirror of the operator surface the reference (SenClaw/sen-mlx) uses
+on its quantized decode/prefill path:
+
+  quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits)
+      mlx_rs::ops::quantized_matmul, called at src/engine/mlx_lm/utils/mod.rs:70-78
+      and from every QuantizedLinear projection (src/engine/mlx_lm/models/llama.rs:195-197,
+      249, 293-294) and tied lm_head (llama.rs:511-517).
+  QuantizedLinear(weight, scales, biases, bias, group_size, bits)
+      nn::QuantizedLinear behind MaybeQuantized<Linear> (llama.rs:115-126, 262-271);
+      forward = quantized_matmul, then + bias when the Linear had one (llama.rs:139-147).
+  dequantize(w, scales, biases, group_size, bits)
+      mlx_rs::ops::dequantize as used at src/engine/mlx_lm/utils/moe.rs:118-126.
+
+Errors are raised as MiqmmError, the counterpart of mlx-rs's Exception built from
+a nonzero mlx-c status (moe.rs:66-76).  Every call goes through libmiqmm.so;
+there is no CPU fallback: if the library is missing the import-time loader
+raises.  torch provides device memory and the current HIP stream only.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+__all__ = [
+    "MiqmmError", "quantized_matmul", "quantized_linear", "QuantizedLinear", "dequantize",
+    "unpack", "synth_problem", "query_route", "result_type", "lib", "LIB_PATH",
+    "OK", "EINVAL", "ENOTSUP", "EHIP", "ROUTE_AUTO", "ROUTE_QMV", "ROUTE_QMM",
+]
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmiqmm.so")
+
+OK, EINVAL, ENOTSUP, EHIP = 0, 1, 2, 3
+ROUTE_AUTO, ROUTE_QMV, ROUTE_QMM = 0, 1, 2
+DT_BF16, DT_F16, DT_F32 = 0, 1, 2
+
+_DT = {torch.bfloat16: DT_BF16, torch.float16: DT_F16, torch.float32: DT_F32}
+
+
+class MiqmmError(RuntimeError):
+    """a nonzero miqmm_status, with the library's message"""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"miqmm status {status}: {message}")
+        self.status = status
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """the loaded libmiqmm.so (raises if it has not been built)"""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing; build it with `python sen-mlx_amd/build.py`")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I64, I, U64 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint64
+    L.miqmm_quantized_matmul.argtypes = [P, P, P, P, P, I64, I64, I64, I, I, I, I, I, I, P]
+    L.miqmm_quantized_matmul_ex.argtypes = [P, P, P, P, P, I64, I64, I64, I, I, I, I, I, I, I, P]
+    L.miqmm_quantized_linear.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I, I, P]
+    L.miqmm_dequantize.argtypes = [P, P, P, P, I64, I64, I, I, I, I, P]
+    L.miqmm_unpack.argtypes = [P, P, I64, I64, I, P]
+    L.miqmm_query_route.argtypes = [I64, I64, I64, I, I, ctypes.POINTER(I), ctypes.POINTER(I)]
+    L.miqmm_synth_problem.argtypes = [P, P, P, P, I64, I64, I64, I, I, I, I, U64, U64, P]
+    for name in ("miqmm_quantized_matmul", "miqmm_quantized_matmul_ex", "miqmm_quantized_linear",
+                 "miqmm_dequantize", "miqmm_unpack", "miqmm_query_route", "miqmm_synth_problem"):
+        getattr(L, name).restype = I
+    L.miqmm_last_error.argtypes, L.miqmm_last_error.restype = [], ctypes.c_char_p
+    L.miqmm_version.argtypes, L.miqmm_version.restype = [], ctypes.c_char_p
+    _lib = L
+    return L
+
+
+def _check(status: int) -> None:
+    if status != OK:
+        raise MiqmmError(status, lib().miqmm_last_error().decode())
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype not in _DT:
+        raise MiqmmError(ENOTSUP, f"dtype {t.dtype} not supported")
+    return _DT[t.dtype]
+
+
+def result_type(x_dtype: torch.dtype, scale_dtype: torch.dtype) -> torch.dtype:
+    """MLX type promotion of (x, scales, biases): equal dtypes are kept, and
+    bfloat16 with float16 (or anything with float32) promotes to float32."""
+    if x_dtype == scale_dtype:
+        return x_dtype
+    return torch.float32
+
+
+def _check_weights(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int,
+                   bits: int):
+    if w.dim() != 2 or scales.dim() != 2 or biases.shape != scales.shape:
+        raise MiqmmError(EINVAL, f"w {tuple(w.shape)} and scales/biases {tuple(scales.shape)}/"
+                                 f"{tuple(biases.shape)} must be 2-D with equal scales/biases shapes")
+    if w.dtype not in (torch.int32, torch.uint32):
+        raise MiqmmError(EINVAL, f"w must hold uint32 words (int32/uint32 tensor), got {w.dtype}")
+    if bits not in (4, 8):
+        raise MiqmmError(ENOTSUP if bits in (2, 3, 5, 6) else EINVAL, f"bits={bits} not provided")
+    N = w.shape[0]
+    K = w.shape[1] * 32 // bits
+    if scales.shape != (N, K // max(group_size, 1)):
+        raise MiqmmError(EINVAL, f"scales shape {tuple(scales.shape)} != ({N}, {K}/{group_size})")
+    for t in (w, scales, biases):
+        if not t.is_contiguous():
+            raise MiqmmError(EINVAL, "w, scales and biases must be contiguous")
+    return N, K
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                     transpose: bool = True, group_size: int = 64, bits: int = 4, *,
+                     out: Optional[torch.Tensor] = None, route: int = ROUTE_AUTO,
+                     stream=None, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y[..., N] = x[..., K] @ dequant(w, scales, biases).T  (transpose=True)
+
+    Argument order and meaning follow mlx_rs::ops::quantized_matmul
+    (src/engine/mlx_lm/utils/mod.rs:70-78).  x's leading dims are flattened into M.
+    The output dtype is MLX's result type of (x, scales, biases)."""
+    N, K = _check_weights(w, scales, biases, group_size, bits)
+    if x.shape[-1] != K:
+        raise MiqmmError(EINVAL, f"x inner dim {x.shape[-1]} != K={K} implied by w {tuple(w.shape)}")
+    xc = x.contiguous()
+    M = xc.numel() // K
+    ydt = result_type(x.dtype, scales.dtype)
+    shape = tuple(x.shape[:-1]) + (N,)
+    if out is None:
+        out = torch.empty(shape, dtype=ydt, device=x.device)
+    elif out.shape != shape or not out.is_contiguous():
+        raise MiqmmError(EINVAL, f"out must be contiguous with shape {shape}")
+    if bias is not None:
+        if bias.shape != (N,) or bias.dtype != out.dtype:
+            raise MiqmmError(EINVAL, f"bias must be [{N}] of dtype {out.dtype}")
+        _check(lib().miqmm_quantized_linear(_ptr(out), _ptr(xc), _ptr(w), _ptr(scales), _ptr(biases),
+                                            _ptr(bias.contiguous()), M, N, K, group_size, bits, _dt(xc),
+                                            _dt(scales), _dt(out), _stream(stream)))
+        return out
+    _check(lib().miqmm_quantized_matmul_ex(_ptr(out), _ptr(xc), _ptr(w), _ptr(scales), _ptr(biases), M, N,
+                                           K, int(bool(transpose)), group_size, bits, _dt(xc), _dt(scales),
+                                           _dt(out), route, _stream(stream)))
+    return out
+
+
+def quantized_linear(x, w, scales, biases, bias=None, group_size: int = 64, bits: int = 4, **kw):
+    """QuantizedLinear forward: quantized_matmul, then + bias (two roundings, as two MLX ops)"""
+    return quantized_matmul(x, w, scales, biases, True, group_size, bits, bias=bias, **kw)
+
+
+class QuantizedLinear:
+    """nn::QuantizedLinear: the swap-in slot of MaybeQuantized<Linear>
+    (src/engine/mlx_lm/models/llama.rs:115-126).  Holds the packed weight
+    [out, in*bits/32], scales/biases [out, in/group_size] and an optional
+    bias [out]; calling it runs quantized_matmul (+ bias)."""
+
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 bias: Optional[torch.Tensor] = None, group_size: int = 64, bits: int = 4):
+        self.out_features, self.in_features = _check_weights(weight, scales, biases, group_size, bits)
+        self.weight, self.scales, self.biases, self.bias = weight, scales, biases, bias
+        self.group_size, self.bits = group_size, bits
+
+    def __call__(self, x: torch.Tensor, **kw) -> torch.Tensor:
+        return self.forward(x, **kw)
+
+    def forward(self, x: torch.Tensor, **kw) -> torch.Tensor:
+        return quantized_matmul(x, self.weight, self.scales, self.biases, True, self.group_size,
+                                self.bits, bias=self.bias, **kw)
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int = 64,
+               bits: int = 4, dtype: Optional[torch.dtype] = None, stream=None) -> torch.Tensor:
+    """out[N, K] = scales * q + biases per group (mlx_rs::ops::dequantize)"""
+    N, K = _check_weights(w, scales, biases, group_size, bits)
+    out = torch.empty((N, K), dtype=dtype or scales.dtype, device=w.device)
+    _check(lib().miqmm_dequantize(_ptr(out), _ptr(w), _ptr(scales), _ptr(biases), N, K, group_size, bits,
+                                  _dt(scales), _dt(out), _stream(stream)))
+    return out
+
+
+def unpack(w: torch.Tensor, bits: int, stream=None) -> torch.Tensor:
+    """codes[N, K] uint8 of packed words w[N, K*bits/32]"""
+    N = w.shape[0]
+    K = w.shape[1] * 32 // bits
+    out = torch.empty((N, K), dtype=torch.uint8, device=w.device)
+    _check(lib().miqmm_unpack(_ptr(out), _ptr(w.contiguous()), N, K, bits, _stream(stream)))
+    return out
+
+
+def synth_problem(M: int, N: int, K: int, group_size: int = 64, bits: int = 4,
+                  x_dtype: torch.dtype = torch.bfloat16, sb_dtype: torch.dtype = torch.bfloat16,
+                  seed: int = 0, stream_id: int = 0, device="cuda", with_x: bool = True,
+                  stream=None):
+    """seeded synthetic (x, w, scales, biases) generated on the device"""
+    x = torch.empty((M, K), dtype=x_dtype, device=device) if with_x else None
+    w = torch.empty((N, K * bits // 32), dtype=torch.int32, device=device)
+    s = torch.empty((N, K // group_size), dtype=sb_dtype, device=device)
+    b = torch.empty_like(s)
+    _check(lib().miqmm_synth_problem(_ptr(x), _ptr(w), _ptr(s), _ptr(b), M, N, K, group_size, bits,
+                                     _DT[x_dtype], _DT[sb_dtype], seed, stream_id, _stream(stream)))
+    return x, w, s, b
+
+
+def query_route(M: int, N: int, K: int, group_size: int = 64, bits: int = 4):
+    """(route, tile info) the dispatcher picks; host only"""
+    route = ctypes.c_int(0)
+    tiles = (ctypes.c_int * 4)()
+    _check(lib().miqmm_query_route(M, N, K, group_size, bits, ctypes.byref(route), tiles))
+    return route.value, tuple(tiles)
+
+
+def version() -> str:
+    return lib().miqmm_version().decode()

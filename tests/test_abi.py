@@ -1,0 +1,121 @@
+"""CPU tests of the C ABI (include/miqmm.h): the library loads, exports every
+declared function, and rejects invalid arguments on the host before touching
+a GPU, with mlx-c's status convention (0 ok, nonzero + message;
+src/engine/mlx_lm/utils/moe.rs:66-76).  No compute call runs here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "miqmm.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(miqmm_[a-z_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import miqmm
+
+    return miqmm.lib()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = _declared()
+    assert {"miqmm_quantized_matmul", "miqmm_quantized_linear", "miqmm_dequantize",
+            "miqmm_unpack", "miqmm_last_error"} <= set(names)
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in miqmm.h but not exported"
+
+
+def test_version(lib):
+    import miqmm
+
+    assert "gfx950" in miqmm.version()
+
+
+def _qmm(lib, **kw):
+    a = dict(y=ctypes.c_void_p(16), x=ctypes.c_void_p(16), w=ctypes.c_void_p(16), s=ctypes.c_void_p(16),
+             b=ctypes.c_void_p(16), M=1, N=64, K=128, transpose=1, g=64, bits=4, xd=0, sd=0, yd=0, route=0)
+    a.update(kw)
+    return lib.miqmm_quantized_matmul_ex(a["y"], a["x"], a["w"], a["s"], a["b"], a["M"], a["N"], a["K"],
+                                         a["transpose"], a["g"], a["bits"], a["xd"], a["sd"], a["yd"],
+                                         a["route"], None)
+
+
+@pytest.mark.parametrize("kw,status,msg", [
+    (dict(transpose=0), 2, "transpose=false"),
+    (dict(bits=3), 2, "bits=3"),
+    (dict(bits=7), 1, "bits must be 4 or 8"),
+    (dict(g=16), 1, "group_size"),
+    (dict(K=96, g=64), 1, "not a multiple of group_size"),
+    (dict(N=0), 1, "N and K"),
+    (dict(K=-64), 1, "N and K"),
+    (dict(M=-1), 1, "M must be"),
+    (dict(xd=1), 2, "x dtype"),
+    (dict(sd=2), 2, "scales/biases dtype"),
+    (dict(yd=7), 1, "y dtype"),
+    (dict(route=9), 1, "route"),
+    (dict(x=ctypes.c_void_p(8)), 1, "16-byte aligned"),
+    (dict(w=ctypes.c_void_p(20)), 1, "16-byte aligned"),
+    (dict(y=None), 1, "null pointer"),
+])
+def test_validation_errors(lib, kw, status, msg):
+    assert _qmm(lib, **kw) == status
+    assert msg in lib.miqmm_last_error().decode()
+
+
+def test_m_zero_is_noop_and_clears_error(lib):
+    assert _qmm(lib, bits=7) == 1
+    assert _qmm(lib, M=0, y=None, x=None) == 0
+    assert lib.miqmm_last_error().decode() == ""
+
+
+def test_other_entry_points_validate(lib):
+    P = ctypes.c_void_p(16)
+    assert lib.miqmm_dequantize(P, P, P, P, 8, 96, 64, 4, 0, 0, None) == 1
+    assert lib.miqmm_dequantize(P, P, P, P, 8, 128, 64, 4, 0, 5, None) == 1
+    assert lib.miqmm_unpack(P, P, 8, 100, 4, None) == 1
+    assert lib.miqmm_unpack(P, P, 8, 128, 2, None) == 1
+    assert lib.miqmm_synth_problem(P, P, P, None, 1, 8, 128, 64, 4, 0, 0, 0, 0, None) == 1
+    assert lib.miqmm_quantized_linear(None, P, P, P, P, None, 1, 8, 128, 64, 4, 0, 0, 0, None) == 1
+
+
+def test_query_route(lib):
+    import miqmm
+
+    for M in (1, 2, 8, 16):
+        route, tiles = miqmm.query_route(M, 14336, 4096, 64, 4)
+        assert route == miqmm.ROUTE_QMV and tiles[0] in (2, 4) and tiles[1] >= M
+    route, tiles = miqmm.query_route(2048, 14336, 4096, 64, 4)
+    assert route == miqmm.ROUTE_QMM and tiles[2] == 64
+    with pytest.raises(miqmm.MiqmmError) as e:
+        miqmm.query_route(1, 64, 96, 64, 4)
+    assert e.value.status == miqmm.EINVAL
+
+
+def test_python_mirror_validation():
+    import torch
+
+    import miqmm
+
+    w = torch.zeros((64, 16), dtype=torch.int32)
+    s = torch.zeros((64, 2), dtype=torch.bfloat16)
+    x = torch.zeros((1, 128), dtype=torch.bfloat16)
+    with pytest.raises(miqmm.MiqmmError, match="inner dim"):
+        miqmm.quantized_matmul(torch.zeros((1, 64), dtype=torch.bfloat16), w, s, s, True, 64, 4)
+    with pytest.raises(miqmm.MiqmmError, match="scales shape"):
+        miqmm.quantized_matmul(x, w, s, s, True, 32, 4)
+    with pytest.raises(miqmm.MiqmmError, match="uint32 words"):
+        miqmm.quantized_matmul(x, w.float(), s, s, True, 64, 4)
+    with pytest.raises(miqmm.MiqmmError) as e:
+        miqmm.quantized_matmul(x, w, s, s, True, 64, 2)
+    assert e.value.status == miqmm.ENOTSUP
+    assert miqmm.result_type(torch.bfloat16, torch.float16) == torch.float32
+    assert miqmm.result_type(torch.bfloat16, torch.bfloat16) == torch.bfloat16
+    lin = miqmm.QuantizedLinear(w, s, s, group_size=64, bits=4)
+    assert (lin.out_features, lin.in_features) == (64, 128)
