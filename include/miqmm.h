@@ -46,7 +46,15 @@ typedef enum {
 
 typedef enum { MIQMM_DT_BF16 = 0, MIQMM_DT_F16 = 1, MIQMM_DT_F32 = 2 } miqmm_dtype;
 
-typedef enum { MIQMM_ROUTE_AUTO = 0, MIQMM_ROUTE_QMV = 1, MIQMM_ROUTE_QMM = 2 } miqmm_route;
+/* QMV: small-M GEMV on MFMA with exact integer codes; QMM: large-M tiled MFMA
+ * with bf16-dequantized W tiles; QMV_DOT: small-M GEMV on v_dot2 (no MFMA),
+ * kept as a selectable alternative to QMV. */
+typedef enum {
+    MIQMM_ROUTE_AUTO = 0,
+    MIQMM_ROUTE_QMV = 1,
+    MIQMM_ROUTE_QMM = 2,
+    MIQMM_ROUTE_QMV_DOT = 3
+} miqmm_route;
 
 /*
  * y = quantized_matmul(x, w, scales, biases, transpose, group_size, bits).
@@ -54,7 +62,8 @@ typedef enum { MIQMM_ROUTE_AUTO = 0, MIQMM_ROUTE_QMV = 1, MIQMM_ROUTE_QMM = 2 } 
  * (reached at src/engine/mlx_lm/utils/mod.rs:70-78 and from every
  * QuantizedLinear::forward).  transpose must be 1; bits in {4, 8};
  * group_size in {32, 64, 128}; K % group_size == 0; x and w 16-byte aligned.
- * M == 0 is a no-op.  Route: M <= 16 -> qmv (HBM-bound GEMV), else qmm (MFMA).
+ * M == 0 is a no-op.  Route: M <= 2 -> qmv_dot, M <= 16 -> qmv (both HBM-bound
+ * GEMVs), else qmm (MFMA-bound tiled matmul).
  */
 int miqmm_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
                            const void* biases, int64_t M, int64_t N, int64_t K, int transpose,
@@ -62,8 +71,9 @@ int miqmm_quantized_matmul(void* y, const void* x, const uint32_t* w, const void
                            void* stream);
 
 /*
- * As miqmm_quantized_matmul, with the route forced (MIQMM_ROUTE_QMV accepts
- * any M, one pass over W per 16 rows of x; MIQMM_ROUTE_QMM any M >= 1).
+ * As miqmm_quantized_matmul, with the route forced (MIQMM_ROUTE_QMV and
+ * MIQMM_ROUTE_QMV_DOT accept any M, one pass over W per 16 rows of x;
+ * MIQMM_ROUTE_QMM any M >= 1).
  * Used by tests to hold both routes to the same oracle on one shape.
  */
 int miqmm_quantized_matmul_ex(void* y, const void* x, const uint32_t* w, const void* scales,
@@ -100,8 +110,10 @@ int miqmm_unpack(uint8_t* codes, const uint32_t* w, int64_t N, int64_t K, int bi
 
 /*
  * Which route and tiling miqmm_quantized_matmul picks for a shape (host
- * only, no GPU access).  route_out: MIQMM_ROUTE_QMV / _QMM.  tile_out[4]:
- * qmv -> {rows per wave, M tile, 0, 0}; qmm -> {BM, BN, BK, 0}.
+ * only, no GPU access).  route_out: a miqmm_route.  tile_out[4]:
+ * qmv -> {16-row tiles per block, M tile, waves per block, 0};
+ * qmv_dot -> {rows per lane group, M tile, lanes per row, 0};
+ * qmm -> {BM, BN, BK, 0}.
  * No reference counterpart: reporting for benches and tests.
  */
 int miqmm_query_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, int* route_out,

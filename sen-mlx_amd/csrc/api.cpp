@@ -58,6 +58,12 @@ int check_launch(hipError_t e, const char* what) {
     return ok();
 }
 
+// M <= 2: the v_dot2 GEMV streams fastest; 3 <= M <= 16: the MFMA GEMV, whose
+// cost barely grows with M; larger M: the tiled MFMA matmul
+int auto_route(int64_t M) {
+    return M <= 2 ? MIQMM_ROUTE_QMV_DOT : M <= 16 ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
+}
+
 int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
                const void* bias, int64_t M, int64_t N, int64_t K, int transpose, int group_size,
                int bits, int x_dtype, int sb_dtype, int y_dtype, int route, void* stream) {
@@ -69,7 +75,8 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
     if (x_dtype != MIQMM_DT_BF16) return fail(MIQMM_ENOTSUP, "x dtype %d not supported (bf16=0)", x_dtype);
     if (y_dtype != MIQMM_DT_BF16 && y_dtype != MIQMM_DT_F16 && y_dtype != MIQMM_DT_F32)
         return fail(MIQMM_EINVAL, "y dtype %d invalid", y_dtype);
-    if (route != MIQMM_ROUTE_AUTO && route != MIQMM_ROUTE_QMV && route != MIQMM_ROUTE_QMM)
+    if (route != MIQMM_ROUTE_AUTO && route != MIQMM_ROUTE_QMV && route != MIQMM_ROUTE_QMM &&
+        route != MIQMM_ROUTE_QMV_DOT)
         return fail(MIQMM_EINVAL, "route %d invalid", route);
     if (M == 0) return ok();
     if (!y || !x || !w || !scales || !biases) return fail(MIQMM_EINVAL, "null pointer argument");
@@ -80,9 +87,9 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
 
     miqmm::QmmArgs a{y, x, w, scales, biases, bias, M, N, K, group_size, bits, x_dtype, sb_dtype, y_dtype,
                      reinterpret_cast<hipStream_t>(stream)};
-    if (route == MIQMM_ROUTE_AUTO) route = M <= 16 ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
-    if (route == MIQMM_ROUTE_QMV) {
-        // the qmv kernel handles at most 16 rows of x per pass over W
+    if (route == MIQMM_ROUTE_AUTO) route = auto_route(M);
+    if (route == MIQMM_ROUTE_QMV || route == MIQMM_ROUTE_QMV_DOT) {
+        // the GEMV kernels handle at most 16 rows of x per pass over W
         for (int64_t m0 = 0; m0 < M; m0 += 16) {
             miqmm::QmmArgs part = a;
             const int64_t mm = M - m0 < 16 ? M - m0 : 16;
@@ -90,7 +97,8 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
             part.x = static_cast<const uint16_t*>(x) + m0 * K;
             const int ysz = y_dtype == MIQMM_DT_F32 ? 4 : 2;
             part.y = static_cast<char*>(y) + m0 * N * ysz;
-            st = check_launch(miqmm::launch_qmv(part), "qmv launch");
+            st = route == MIQMM_ROUTE_QMV ? check_launch(miqmm::launch_qmv_mfma(part), "qmv launch")
+                                          : check_launch(miqmm::launch_qmv(part), "qmv_dot launch");
             if (st != MIQMM_OK) return st;
         }
         return ok();
@@ -158,11 +166,12 @@ int miqmm_query_route(int64_t M, int64_t N, int64_t K, int group_size, int bits,
     a.K = K;
     a.group_size = group_size;
     a.bits = bits;
-    const int route = M <= 16 ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
+    const int route = auto_route(M);
     if (route_out) *route_out = route;
     if (tile_out) {
         tile_out[0] = tile_out[1] = tile_out[2] = tile_out[3] = 0;
-        if (route == MIQMM_ROUTE_QMV) miqmm::qmv_config(a, &tile_out[0], &tile_out[1]);
+        if (route == MIQMM_ROUTE_QMV) miqmm::qmv_mfma_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
+        else if (route == MIQMM_ROUTE_QMV_DOT) miqmm::qmv_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
         else miqmm::qmm_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
     }
     return ok();

@@ -36,7 +36,7 @@ __host__ __device__ __forceinline__ uint64_t stream_key_host(uint64_t seed, uint
 __device__ __forceinline__ float ih_normal(uint64_t r) {
     const int32_t s = (int32_t)(r & 0xffffu) + (int32_t)((r >> 16) & 0xffffu) +
                       (int32_t)((r >> 32) & 0xffffu) + (int32_t)((r >> 48) & 0xffffu);
-    return __fmul_rn((float)(s - 131070), 2.6428997e-05f);
+    return f32_pinned(__fmul_rn((float)(s - 131070), 2.6428997e-05f));
 }
 
 template <int DT>
@@ -49,7 +49,7 @@ template <int DT>
 __global__ void synth_normal_kernel(uint16_t* __restrict__ out, int64_t count, uint64_t key, float sigma) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
-    out[i] = to_half<DT>(__fmul_rn(ih_normal(mix64(key + (uint64_t)i * kGamma)), sigma));
+    out[i] = to_half<DT>(f32_pinned(__fmul_rn(ih_normal(mix64(key + (uint64_t)i * kGamma)), sigma)));
 }
 
 __global__ void synth_codes_kernel(uint32_t* __restrict__ w, int64_t N, int64_t K, int bits, uint64_t key) {
@@ -72,11 +72,11 @@ __global__ void synth_sb_kernel(uint16_t* __restrict__ s, uint16_t* __restrict__
                                 int bits, uint64_t ks, uint64_t kb) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
-    const float sv = __fmul_rn(fabsf(ih_normal(mix64(ks + (uint64_t)i * kGamma))), 0.02f);
+    const float sv = f32_pinned(__fmul_rn(fabsf(ih_normal(mix64(ks + (uint64_t)i * kGamma))), 0.02f));
     const uint16_t sh = to_half<DT>(sv);
     const float sr = half_to_f32<DT>(sh);
-    const float noise = __fmul_rn(ih_normal(mix64(kb + (uint64_t)i * kGamma)), 0.002f);
-    const float bv = __fadd_rn(__fmul_rn(-(float)(1u << (bits - 1)), sr), noise);
+    const float noise = f32_pinned(__fmul_rn(ih_normal(mix64(kb + (uint64_t)i * kGamma)), 0.002f));
+    const float bv = f32_pinned(__fadd_rn(f32_pinned(__fmul_rn(-(float)(1u << (bits - 1)), sr)), noise));
     s[i] = sh;
     b[i] = to_half<DT>(bv);
 }
@@ -97,7 +97,7 @@ __global__ void dequantize_kernel(void* __restrict__ out, const uint32_t* __rest
         const int64_t k = j * per + t;
         const float s = half_to_f32<SBT>(sc[n * G + (k >> gs_shift)]);
         const float b = half_to_f32<SBT>(bi[n * G + (k >> gs_shift)]);
-        const float v = fmaf(s, (float)((word >> (bits * t)) & mask), b);
+        const float v = f32_pinned(fmaf(s, (float)((word >> (bits * t)) & mask), b));
         const int64_t o = n * K + k;
         if (out_dtype == DT_F32) ((float*)out)[o] = v;
         else if (out_dtype == DT_F16) ((uint16_t*)out)[o] = f32_to_f16_bits(v);

@@ -19,6 +19,14 @@ typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
 enum : int { DT_BF16 = 0, DT_F16 = 1, DT_F32 = 2 };
 
+// Materialises an fp32 value in a register.  Without it the backend may fuse
+// the multiply or add that produced it with a following fp16 conversion into
+// one v_fma_mixlo_f16, which rounds once where fp32-then-fp16 rounds twice.
+__device__ __forceinline__ float f32_pinned(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // ---------------------------------------------------------------- conversions
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
@@ -49,8 +57,9 @@ __device__ __forceinline__ void store_out(void* y, int64_t idx, int y_dtype, flo
         if (bias) v += ((const float*)bias)[bidx];
         ((float*)y)[idx] = v;
     } else if (y_dtype == DT_F16) {
-        uint16_t h = f32_to_f16_bits(v);
-        if (bias) h = f32_to_f16_bits(f16_bits_to_f32(h) + f16_bits_to_f32(((const uint16_t*)bias)[bidx]));
+        uint16_t h = f32_to_f16_bits(f32_pinned(v));
+        if (bias)
+            h = f32_to_f16_bits(f32_pinned(f16_bits_to_f32(h) + f16_bits_to_f32(((const uint16_t*)bias)[bidx])));
         ((uint16_t*)y)[idx] = h;
     } else {
         uint16_t h = f32_to_bf16_bits(v);
@@ -71,12 +80,61 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a), as_bf16x2(b), c, false);
 }
 
-// word of eight 4-bit codes -> four bf16 pairs (q_j+128, q_{j+4}+128), j=0..3
-__device__ __forceinline__ void unpack4_magic(uint32_t w, uint32_t p[4]) {
-    p[0] = (w & 0x000F000Fu) | kMagic128x2;
-    p[1] = ((w >> 4) & 0x000F000Fu) | kMagic128x2;
-    p[2] = ((w >> 8) & 0x000F000Fu) | kMagic128x2;
-    p[3] = ((w >> 12) & 0x000F000Fu) | kMagic128x2;
+// (a & mask) | magic.  With `mask` held in a VGPR (see vgpr_const) and `magic`
+// a constant this selects one v_and_or_b32; with both as constants gfx950's
+// single constant-bus operand forces an and plus an or.  Written in C, not
+// inline asm, so the hazard recognizer sees the result register when an MFMA
+// consumes it (an MFMA reading a VALU result needs wait states the compiler
+// only inserts for instructions it can see).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
+    return (a & mask) | magic;
+}
+
+// a constant materialised in a VGPR once, opaque to constant folding
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+    uint32_t v;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "i"(c));
+    return v;
+}
+
+// word of eight 4-bit codes -> four bf16 pairs (q_j+128, q_{j+4}+128), j=0..3;
+// mask and magic are passed in registers (0x000F000F, 0x43004300)
+__device__ __forceinline__ void unpack4_magic(uint32_t w, uint32_t p[4], uint32_t mask, uint32_t magic) {
+    p[0] = and_or(w, mask, magic);
+    p[1] = and_or(w >> 4, mask, magic);
+    p[2] = and_or(w >> 8, mask, magic);
+    p[3] = and_or(w >> 12, mask, magic);
+}
+
+// ---------------------------------------------------------------- buffer loads
+// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes
+// return zero, which the kernels use to mask ragged rows and chunks.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+constexpr uint32_t kOOB = 0x80000000u;  // an offset past any resource this library builds
+
+__device__ __forceinline__ u32x4_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint16_t bload2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+// ---------------------------------------------------------------- reductions
+// Sum over groups of L consecutive lanes (L = 16, 32 or 64) with DPP moves.
+// Afterwards lanes li >= L-16 of each group (li = lane % L) hold the group sum.
+template <int L>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    if constexpr (L >= 32)  // row_bcast15 into rows 1 and 3
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
+    if constexpr (L >= 64)  // row_bcast31 into rows 2 and 3
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
+    return v;
 }
 
 // x words (x0|x1, x2|x3, x4|x5, x6|x7) -> pairs (x_j, x_{j+4}) matching unpack4_magic

@@ -20,11 +20,13 @@ struct QmmArgs {
 };
 
 // route launchers; return hipSuccess or the launch error
-hipError_t launch_qmv(const QmmArgs& a);
+hipError_t launch_qmv(const QmmArgs& a);       // VALU dot2 GEMV
+hipError_t launch_qmv_mfma(const QmmArgs& a);  // group-diagonal MFMA GEMV
 hipError_t launch_qmm(const QmmArgs& a);
 
-// qmv tiling used for a given problem (rows per wave, M tile); for reporting
-void qmv_config(const QmmArgs& a, int* rows_per_wave, int* m_tile);
+// tiling used for a given problem; for reporting
+void qmv_config(const QmmArgs& a, int* rows_per_subgroup, int* m_tile, int* lanes_per_row);
+void qmv_mfma_config(const QmmArgs& a, int* tiles_per_block, int* m_tile, int* waves_per_block);
 void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk);
 
 hipError_t launch_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,

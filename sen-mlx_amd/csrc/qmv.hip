@@ -7,30 +7,46 @@
 // src/engine/mlx_lm/models/llama.rs:195-197,249,293-294) during decode, where
 // x is one token (M=1) or a handful of speculative/batched rows.
 //
-// HBM-bound design (no MFMA): a wave owns RPS output rows n; lane l streams the
-// 16-byte chunks l, l+64, ... of each of those rows, so every load instruction
-// of the wave reads 1 KiB of one row contiguously.  A chunk holds 32 (4-bit)
-// or 16 (8-bit) codes and always lies inside one quantization group, so its
-// scale and bias are two scalars per row.  Codes become exact bf16 operands
-// (4-bit: 0x4300|q = 128+q; 8-bit: top half of the fp32 value) and are dotted
-// with x by v_dot2_f32_bf16 in fp32.  Per chunk the dequant is applied in
-// factorised form, exactly:
+// HBM-bound design (no MFMA).  A row of W is a sequence of C 16-byte chunks
+// (32 4-bit or 16 8-bit codes each; a chunk never straddles a quantization
+// group).  A wave is split into 64/L sub-groups of L lanes; a sub-group owns R
+// rows at a time and its lane li streams chunks li, li+L, ... of those rows,
+// so each load instruction reads L*16 contiguous bytes of each row.  L is
+// chosen per K so that few lanes idle (K=896: 28 chunks -> L=32).
+//
+// Waves are persistent: a wave walks row tiles tile, tile+nwaves, ... and the
+// (tile, chunk) iterations are software-pipelined one deep: the next
+// iteration's codes, scales, biases and x are in flight while the current one
+// is computed, so a wave keeps ~R*16 bytes per lane outstanding at all times.
+//
+// Arithmetic: codes become exact bf16 operands (4-bit: 0x4300|q = 128+q;
+// 8-bit: the top half of the fp32 value of q) and are dotted with x by
+// v_dot2_f32_bf16 in fp32.  Per chunk the dequant is applied in factorised
+// form, exactly:
 //     sum_k x_k (s q_k + b) = s * sum_k x_k (q_k + c) + (b - c s) * sum_k x_k
-// with c = 128 for 4-bit, 0 for 8-bit.  The 64 lane partials of each output
-// are summed with a butterfly across the wave.
+// with c = 128 (4-bit) or 0 (8-bit).  Lane partials of one row are summed with
+// a butterfly over its L lanes.
 #include "miqmm_device.h"
 #include "miqmm_internal.h"
 
 namespace miqmm {
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+constexpr int kMaxBlocksPerCU = 8;
+constexpr int kNumCUs = 256;
 
-template <int BITS, int SBT, int MT, int RPS>
+// one pipeline stage: the codes, scales and biases of R rows at one chunk
+// position, and (when XPF) the matching x chunk of every row of x
+template <int BITS, int R, int MT, bool XPF>
+struct Stage {
+    static constexpr int NP = (128 / BITS) / 2;  // bf16 pairs of x per chunk
+    u32x4_t q[R];
+    uint16_t s[R], b[R];
+    uint32_t xw[XPF ? MT : 1][NP];
+    uint32_t xoff;  // byte offset of this chunk in row 0 of x, or kOOB past the row end
+};
+
+template <int BITS, int SBT, int MT, int L, int R>
 __global__ __launch_bounds__(256) void qmv_kernel(const uint16_t* __restrict__ x,
                                                   const uint32_t* __restrict__ w,
                                                   const uint16_t* __restrict__ sc,
@@ -39,114 +55,164 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint16_t* __restrict__ x
                                                   int M, int N, int K, int gs_shift, int y_dtype) {
     constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk: 32 or 16
     constexpr int CPC = 1 << CPC_SHIFT;
-    constexpr int NP = CPC / 2;                   // bf16 pairs per chunk
+    constexpr int NP = CPC / 2;
+    constexpr int SG = 64 / L;                    // sub-groups (row slots) per wave
+    constexpr int TILE = SG * R;                  // rows per wave tile
+    constexpr bool XPF = MT <= 2;                 // prefetch x with the codes (registers allow it)
+    using St = Stage<BITS, R, MT, XPF>;
+
     const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPS;
-    if (row0 >= N) return;  // wave-uniform
+    const int sg = lane / L, li = lane % L;
+    // wave index, made provably wave-uniform so tile bases live in SGPRs
+    const int gwave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    const int nwaves = gridDim.x * 4;
     const int C = K >> CPC_SHIFT;
-    const int64_t KW = (int64_t)K * BITS / 32;
+    const int J = (C + L - 1) / L;  // chunk iterations per row
+    const int tiles = (N + TILE - 1) / TILE;
+    const int my_tiles = gwave < tiles ? (tiles - 1 - gwave) / nwaves + 1 : 0;
+    const int iters = my_tiles * J;
+    if (iters == 0) return;  // wave-uniform
+    const uint32_t row_bytes = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
+    const uint32_t xrow_bytes = (uint32_t)K * 2;
+    const auto xr = make_rsrc(x, (uint32_t)M * xrow_bytes);
+    const uint32_t kMask = vgpr_const(0x000F000Fu), kMagic = kMagic128x2;
 
-    const uint32_t* wrow[RPS];
-    int64_t srow[RPS];
+    // x of one chunk position for every row of x (zero past the row end or m >= M)
+    auto load_x = [&](uint32_t xoff, uint32_t (*xw)[NP]) {
 #pragma unroll
-    for (int r = 0; r < RPS; ++r) {
-        const int n = min(row0 + r, N - 1);
-        wrow[r] = w + (int64_t)n * KW;
-        srow[r] = (int64_t)n * G;
-    }
+        for (int m = 0; m < MT; ++m) {
+            const uint32_t off = m < M ? xoff + (uint32_t)m * xrow_bytes : kOOB;
+#pragma unroll
+            for (int i = 0; i < NP / 4; ++i) {
+                const u32x4_t v = bload16(xr, off + i * 16);
+                xw[m][4 * i + 0] = v[0];
+                xw[m][4 * i + 1] = v[1];
+                xw[m][4 * i + 2] = v[2];
+                xw[m][4 * i + 3] = v[3];
+            }
+        }
+    };
+    // x sums and (4-bit) the pairing (x_j, x_{j+4}) matching unpack4_magic
+    auto prep_x = [&](const uint32_t (*xw)[NP], uint32_t (*X)[NP], float* xs) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            xs[m] = 0.f;
+#pragma unroll
+            for (int i = 0; i < NP; ++i) xs[m] = dot2(xw[m][i], kOnesBf16x2, xs[m]);
+            if constexpr (BITS == 4) {
+#pragma unroll
+                for (int wi = 0; wi < 4; ++wi) perm_x_for4(&xw[m][4 * wi], &X[m][4 * wi]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < NP; ++i) X[m][i] = xw[m][i];
+            }
+        }
+    };
 
-    float acc[RPS][MT];
+    // (tile, chunk iteration) of the next stage to issue and of the stage being computed
+    int tile_i = gwave, j_i = 0, tile_c = gwave, j_c = 0;
+    auto issue = [&](St& st) {
+        const int tile = tile_i;
+        const int c = li + j_i * L;
+        if (++j_i == J) {
+            j_i = 0;
+            tile_i += nwaves;
+        }
+        const int rows_left = N - tile * TILE;
+        const uint32_t valid_rows = (uint32_t)(rows_left < TILE ? rows_left : TILE);
+        // resources rebased on the tile: 32-bit offsets, and rows past N read as zero
+        const auto wr = make_rsrc((const char*)w + (size_t)tile * TILE * row_bytes, valid_rows * row_bytes);
+        const auto sr = make_rsrc(sc + (size_t)tile * TILE * G, valid_rows * G * 2);
+        const auto br = make_rsrc(bi + (size_t)tile * TILE * G, valid_rows * G * 2);
+        const bool cv = c < C;
+        const uint32_t g = (uint32_t)((c << CPC_SHIFT) >> gs_shift);
 #pragma unroll
-    for (int r = 0; r < RPS; ++r)
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = (uint32_t)(sg * R + r);
+            st.q[r] = bload16(wr, cv ? row * row_bytes + (uint32_t)c * 16 : kOOB);
+            st.s[r] = bload2(sr, (row * G + g) * 2);
+            st.b[r] = bload2(br, (row * G + g) * 2);
+        }
+        st.xoff = cv ? (uint32_t)c * CPC * 2 : kOOB;
+        if constexpr (XPF) load_x(st.xoff, st.xw);
+    };
+
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
 
-    // one chunk of prefetch: the next chunk's codes are in flight while the
-    // current one is computed
-    u32x4_t qn[RPS];
-    int c = lane;
-    if (c < C) {
-#pragma unroll
-        for (int r = 0; r < RPS; ++r) qn[r] = ldg16(wrow[r] + c * 4);
-    }
-    for (; c < C; c += 64) {
-        u32x4_t q[RPS];
-#pragma unroll
-        for (int r = 0; r < RPS; ++r) q[r] = qn[r];
-        if (c + 64 < C) {
-#pragma unroll
-            for (int r = 0; r < RPS; ++r) qn[r] = ldg16(wrow[r] + (c + 64) * 4);
+    auto compute = [&](const St& st) {
+        uint32_t X[MT][NP];
+        float xs[MT];
+        if constexpr (XPF) {
+            prep_x(st.xw, X, xs);
+        } else {
+            uint32_t xw[MT][NP];
+            load_x(st.xoff, xw);
+            prep_x(xw, X, xs);
         }
-        const int g = (c << CPC_SHIFT) >> gs_shift;
-        float s[RPS], bb[RPS];
 #pragma unroll
-        for (int r = 0; r < RPS; ++r) {
-            s[r] = half_to_f32<SBT>(sc[srow[r] + g]);
-            bb[r] = half_to_f32<SBT>(bi[srow[r] + g]);
-            if constexpr (BITS == 4) bb[r] = fmaf(-128.f, s[r], bb[r]);
-        }
-        uint32_t p[RPS][NP];
-#pragma unroll
-        for (int r = 0; r < RPS; ++r)
+        for (int r = 0; r < R; ++r) {
+            uint32_t p[NP];
 #pragma unroll
             for (int wi = 0; wi < 4; ++wi) {
-                if constexpr (BITS == 4) unpack4_magic(q[r][wi], &p[r][wi * 4]);
-                else unpack8_pairs(q[r][wi], &p[r][wi * 2]);
+                if constexpr (BITS == 4) unpack4_magic(st.q[r][wi], &p[wi * 4], kMask, kMagic);
+                else unpack8_pairs(st.q[r][wi], &p[wi * 2]);
             }
-        const uint16_t* xc = x + (int64_t)c * CPC;
+            const float s = half_to_f32<SBT>(st.s[r]);
+            float b = half_to_f32<SBT>(st.b[r]);
+            if constexpr (BITS == 4) b = fmaf(-128.f, s, b);
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            if (m < M) {
-                uint32_t xw[NP];
+            for (int m = 0; m < MT; ++m) {
+                float a = 0.f;
 #pragma unroll
-                for (int i = 0; i < NP / 4; ++i) {
-                    u32x4_t v = ldg16(xc + (int64_t)m * K + i * 8);
-                    xw[4 * i + 0] = v[0];
-                    xw[4 * i + 1] = v[1];
-                    xw[4 * i + 2] = v[2];
-                    xw[4 * i + 3] = v[3];
-                }
-                float xs = 0.f;
-#pragma unroll
-                for (int i = 0; i < NP; ++i) xs = dot2(xw[i], kOnesBf16x2, xs);
-                uint32_t X[NP];
-                if constexpr (BITS == 4) {
-#pragma unroll
-                    for (int wi = 0; wi < 4; ++wi) perm_x_for4(&xw[4 * wi], &X[4 * wi]);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < NP; ++i) X[i] = xw[i];
-                }
-#pragma unroll
-                for (int r = 0; r < RPS; ++r) {
-                    float a = 0.f;
-#pragma unroll
-                    for (int i = 0; i < NP; ++i) a = dot2(X[i], p[r][i], a);
-                    acc[r][m] = fmaf(s[r], a, acc[r][m]);
-                    acc[r][m] = fmaf(bb[r], xs, acc[r][m]);
-                }
+                for (int i = 0; i < NP; ++i) a = dot2(X[m][i], p[i], a);
+                acc[r][m] = fmaf(s, a, acc[r][m]);
+                acc[r][m] = fmaf(b, xs[m], acc[r][m]);
             }
         }
-    }
+        if (++j_c == J) {  // tile complete: reduce over the sub-group and store
+            const int row0 = tile_c * TILE + sg * R;
+            j_c = 0;
+            tile_c += nwaves;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const float v = lane_group_sum<L>(acc[r][m]);
+                    acc[r][m] = 0.f;
+                    const int n = row0 + r;
+                    if (li == L - 16 + ((r * MT + m) & 15) && m < M && n < N)
+                        store_out(y, (int64_t)m * N + n, y_dtype, v, bias, n);
+                }
+        }
+    };
 
-#pragma unroll
-    for (int r = 0; r < RPS; ++r)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            const float v = wave_sum(acc[r][m]);
-            const int n = row0 + r;
-            if (lane == ((r * MT + m) & 63) && m < M && n < N)
-                store_out(y, (int64_t)m * N + n, y_dtype, v, bias, n);
-        }
+    // one-deep software pipeline over (tile, chunk) iterations, ping-ponging
+    // between two stages so no stage is ever copied
+    St A, B;
+    issue(A);
+    if (iters > 1) issue(B);
+    for (int it = 0; it < iters; it += 2) {
+        if (it > 0 && it + 1 < iters) issue(B);
+        compute(A);
+        if (it + 1 >= iters) break;
+        if (it + 2 < iters) issue(A);
+        compute(B);
+    }
 }
 
-template <int BITS, int SBT, int MT, int RPS>
+template <int BITS, int SBT, int MT, int L, int R>
 hipError_t launch_t(const QmmArgs& a) {
-    const int rows_per_block = 4 * RPS;
-    const int blocks = (int)((a.N + rows_per_block - 1) / rows_per_block);
+    constexpr int TILE = (64 / L) * R;
+    const int64_t tiles = (a.N + TILE - 1) / TILE;
+    const int64_t want = (tiles + 3) / 4;
+    const int blocks = (int)(want < kNumCUs * kMaxBlocksPerCU ? want : kNumCUs * kMaxBlocksPerCU);
     const int gs_shift = __builtin_ctz((unsigned)a.group_size);
-    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, RPS>), dim3(blocks), dim3(256), 0, a.stream,
+    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R>), dim3(blocks), dim3(256), 0, a.stream,
                        (const uint16_t*)a.x, a.w, (const uint16_t*)a.scales,
                        (const uint16_t*)a.biases, a.y, a.bias, (int)a.M, (int)a.N, (int)a.K,
                        gs_shift, a.y_dtype);
@@ -155,30 +221,52 @@ hipError_t launch_t(const QmmArgs& a) {
 
 int pick_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
-// 4 rows per wave unless that leaves fewer than 2 blocks per CU on 256 CUs
-int pick_rps(int64_t N) { return (N + 15) / 16 >= 512 ? 4 : 2; }
+// lanes per row: the largest of 64/32/16 whose ragged last pass idles at
+// most an eighth of the lanes, else the one idling the fewest
+int pick_l(int64_t K, int bits) {
+    const int64_t C = K * bits / 128;
+    int best = 64;
+    int64_t best_waste = -1;
+    for (int L : {64, 32, 16}) {
+        const int64_t waste = ((C + L - 1) / L) * L - C;
+        if (waste * 8 <= ((C + L - 1) / L) * L) return L;
+        if (best_waste < 0 || waste < best_waste) {
+            best = L;
+            best_waste = waste;
+        }
+    }
+    return best;
+}
 
-template <int BITS, int SBT, int MT>
-hipError_t launch_rps(const QmmArgs& a) {
-    return pick_rps(a.N) == 4 ? launch_t<BITS, SBT, MT, 4>(a) : launch_t<BITS, SBT, MT, 2>(a);
+// rows per sub-group: fewer as M grows (registers for x and accumulators)
+int pick_r(int64_t M) { return M <= 2 ? 4 : M <= 4 ? 2 : 1; }
+
+template <int BITS, int SBT, int MT, int R>
+hipError_t launch_l(const QmmArgs& a) {
+    switch (pick_l(a.K, a.bits)) {
+        case 16: return launch_t<BITS, SBT, MT, 16, R>(a);
+        case 32: return launch_t<BITS, SBT, MT, 32, R>(a);
+        default: return launch_t<BITS, SBT, MT, 64, R>(a);
+    }
 }
 
 template <int BITS, int SBT>
 hipError_t launch_mt(const QmmArgs& a) {
     switch (pick_mt(a.M)) {
-        case 1: return launch_rps<BITS, SBT, 1>(a);
-        case 2: return launch_rps<BITS, SBT, 2>(a);
-        case 4: return launch_rps<BITS, SBT, 4>(a);
-        case 8: return launch_rps<BITS, SBT, 8>(a);
-        default: return launch_rps<BITS, SBT, 16>(a);
+        case 1: return launch_l<BITS, SBT, 1, 4>(a);
+        case 2: return launch_l<BITS, SBT, 2, 4>(a);
+        case 4: return launch_l<BITS, SBT, 4, 2>(a);
+        case 8: return launch_l<BITS, SBT, 8, 1>(a);
+        default: return launch_l<BITS, SBT, 16, 1>(a);
     }
 }
 
 }  // namespace
 
-void qmv_config(const QmmArgs& a, int* rows_per_wave, int* m_tile) {
-    if (rows_per_wave) *rows_per_wave = pick_rps(a.N);
+void qmv_config(const QmmArgs& a, int* rows_per_subgroup, int* m_tile, int* lanes_per_row) {
+    if (rows_per_subgroup) *rows_per_subgroup = pick_r(a.M);
     if (m_tile) *m_tile = pick_mt(a.M);
+    if (lanes_per_row) *lanes_per_row = pick_l(a.K, a.bits);
 }
 
 hipError_t launch_qmv(const QmmArgs& a) {

@@ -1,0 +1,325 @@
+// qmv_mfma.hip -- small-M route (M = 1..16) of affine group-quantized matmul on
+// bf16 MFMA with exact integer codes.
+//
+//   y[m, n] = sum_k x[m, k] * (s[n, g(k)] * q[n, k] + b[n, g(k)])   (transpose=true)
+//
+// The reference reaches this through its quantized projections during decode
+// (src/engine/mlx_lm/utils/mod.rs:70-78; src/engine/mlx_lm/models/llama.rs:
+// 195-197,249,293-294,511-517) with x of one token, or a few rows when
+// verifying speculative tokens.
+//
+// Why MFMA for a bandwidth-bound GEMV: the VALU cost of unpacking codes and
+// dotting them with x is what keeps a VALU GEMV from streaming at HBM speed;
+// here the dot products run on the matrix cores and the VALU only unpacks.
+//
+// v_mfma_f32_16x16x32_bf16 computes D[16 x 16] += A[16 x 32] * B[32 x 16].
+//   B: 32 codes (one "k-block") of 16 rows n of W, as exact bf16 values 128+q
+//      (4-bit: bits 0x4300|q) or q (8-bit: top half of the fp32 value).
+//   A: the matching 32 values of x, one copy per MFMA row that is live for
+//      this k-block.  MFMA rows are "group slots": row r = (m, slot) with
+//      m = r / GS, slot = r % GS, GS = 16 / MT.  The A row of (m, slot) holds
+//      x[m] only for k-blocks whose quantization group g has g % GS == slot,
+//      zero otherwise.  So after GS consecutive groups, D[(m, slot)][n] holds
+//      sum_{k in group} x[m,k] * code[n,k] for GS different groups at once,
+//      and the per-group dequant is applied once per GS groups:
+//        y[m,n] += s[n,g] * D[(m,slot)][n] + (b[n,g] - c*s[n,g]) * X[(m,slot)]
+//      with c = 128 (4-bit) or 0 (8-bit) and X the per-group sums of x, taken
+//      by one more MFMA of A against an all-ones B.
+//   This keeps the dequant exact (fp32, as the reference's fp32 fma) and
+//   needs ~1 VALU op per code.
+//
+// Work split: a block owns T tiles of 16 output rows n and all of K; its WPB
+// waves split K into contiguous k-quad ranges (a k-quad is 4 k-blocks = 128
+// codes) and combine their partial sums through LDS at the end.
+//
+// Loads: 4-bit -- lane (n, q) loads 16 bytes = chunk 4u+q (k-block 4u+q) of
+// row n, so the 4 lanes of a row read 64 contiguous bytes; a 4x4 transpose of
+// words across the lane quarters (v_permlane32_swap, v_permlane16_swap) then
+// gives lane (n, q) quad q of each of the four k-blocks, which is what the B
+// operand layout wants.  8-bit -- lane (n, q) loads quad q (8 bytes) of one
+// k-block directly.  All loads are raw buffer loads with 32-bit offsets from
+// per-block bases; offsets past the end read as zero, which masks ragged K,
+// ragged N and the A rows of inactive group slots.
+#include <type_traits>
+
+#include "miqmm_device.h"
+#include "miqmm_internal.h"
+
+namespace miqmm {
+namespace {
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// 4x4 transpose of words across the four 16-lane rows of a wave: afterwards
+// register i of row q holds what register q of row i held
+// (permlane32_swap(a, b) exchanges a's lanes 32-63 with b's lanes 0-31;
+// permlane16_swap(a, b) exchanges a's rows 1 and 3 with b's rows 0 and 2)
+__device__ __forceinline__ void transpose4x4(u32x4_t& v) {
+    auto a = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+    auto b = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+    auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    v[0] = c[0];
+    v[1] = c[1];
+    v[2] = d[0];
+    v[3] = d[1];
+}
+
+template <int BITS, int T>
+struct QStage {
+    // 4-bit: one 16-byte chunk per tile (transposed to 4 k-blocks' quads);
+    // 8-bit: 8 bytes per tile per k-block
+    u32x4_t code[BITS == 4 ? T : 2 * T];
+    u32x4_t xa[4];  // x for the 4 k-blocks (zero unless this lane's slot is live)
+};
+
+template <int BITS, int SBT, int MT, int T, int WPB>
+__global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __restrict__ x,
+                                                            const uint32_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ sc,
+                                                            const uint16_t* __restrict__ bi,
+                                                            void* __restrict__ y,
+                                                            const void* __restrict__ bias, int M, int N,
+                                                            int K, int gs_shift, int y_dtype) {
+    constexpr int GS = 16 / MT;                 // group slots per m
+    constexpr int NMT = MT >= 4 ? MT / 4 : 1;   // distinct m per lane
+    constexpr float kCentre = BITS == 4 ? 128.f : 0.f;
+    using St = QStage<BITS, T>;
+
+    extern __shared__ float red[];  // [WPB][T][64 lanes][NMT]
+
+    const int lane = threadIdx.x & 63;
+    const int nl = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = blockIdx.x * 16 * T;
+    const int KB = K >> 5;            // k-blocks of 32 codes
+    const int KQ = (KB + 3) >> 2;     // k-quads
+    const int QS = (KQ + WPB - 1) / WPB;
+    const int u0 = wv * QS;
+    const int u1 = min(u0 + QS, KQ);
+    const int G = K >> gs_shift;
+    const int cl_shift = gs_shift - 5 + __builtin_ctz(GS);  // log2(k-blocks per GS-group cycle)
+    const uint32_t row_bytes = (uint32_t)K * BITS / 8;
+    const int rows_here = min(16 * T, N - n0);
+    const auto wr = make_rsrc((const char*)w + (size_t)n0 * row_bytes, (uint32_t)rows_here * row_bytes);
+    const auto sr = make_rsrc(sc + (size_t)n0 * G, (uint32_t)rows_here * G * 2);
+    const auto br = make_rsrc(bi + (size_t)n0 * G, (uint32_t)rows_here * G * 2);
+    const auto xr = make_rsrc(x, (uint32_t)M * K * 2);
+    const uint32_t kMask = vgpr_const(0x000F000Fu), kMagic = kMagic128x2;
+
+    // this lane's A row: (m_a, slot_a)
+    const int m_a = nl / GS, slot_a = nl % GS;
+
+    f32x4_t D[T], DX;
+    float tot[T][NMT];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        D[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < NMT; ++i) tot[t][i] = 0.f;
+    }
+    DX = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto issue = [&](int u, St& st) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint32_t row = (uint32_t)(16 * t + nl);
+            if constexpr (BITS == 4) {
+                const int chunk = 4 * u + q;
+                st.code[t] = bload16(wr, chunk < KB ? row * row_bytes + (uint32_t)chunk * 16 : kOOB);
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    // two k-blocks per 16-byte register: quads of k-blocks 4u+2h, 4u+2h+1
+                    const int kb0 = 4 * u + 2 * h;
+                    const uint32_t o0 = kb0 < KB ? row * row_bytes + (uint32_t)kb0 * 32 + q * 8 : kOOB;
+                    const uint32_t o1 = kb0 + 1 < KB ? row * row_bytes + (uint32_t)(kb0 + 1) * 32 + q * 8 : kOOB;
+                    const auto lo = __builtin_amdgcn_raw_buffer_load_b64(wr, o0, 0, 0);
+                    const auto hi = __builtin_amdgcn_raw_buffer_load_b64(wr, o1, 0, 0);
+                    st.code[2 * t + h] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int kb = 4 * u + i;
+            const int gidx = kb >> (gs_shift - 5);
+            const bool live = kb < KB && m_a < M && (gidx % GS) == slot_a;
+            st.xa[i] = bload16(xr, live ? (uint32_t)m_a * K * 2 + (uint32_t)(kb * 32 + 8 * q) * 2 : kOOB);
+        }
+    };
+
+    // apply the dequant of one group cycle c (groups c*GS .. c*GS+GS-1) and clear D
+    auto rescale = [&](int c) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint32_t row = (uint32_t)(16 * t + nl);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = 4 * q + j;
+                const int g = c * GS + (r % GS);
+                const uint32_t off = g < G ? (row * G + g) * 2 : kOOB;
+                const float s = half_to_f32<SBT>(bload2(sr, off));
+                const float b = half_to_f32<SBT>(bload2(br, off)) - kCentre * s;
+                const int mi = GS >= 4 ? 0 : j / GS;  // which of this lane's m (compile time)
+                tot[t][mi] = fmaf(s, D[t][j], tot[t][mi]);
+                tot[t][mi] = fmaf(b, DX[j], tot[t][mi]);
+            }
+            D[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        DX = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    };
+
+    const u32x4_t ones = {kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
+    auto compute = [&](int u, St& st) {
+        if constexpr (BITS == 4) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) transpose4x4(st.code[t]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int kb = 4 * u + i;
+            u32x4_t a;
+            if constexpr (BITS == 4) {
+                uint32_t xw[4] = {st.xa[i][0], st.xa[i][1], st.xa[i][2], st.xa[i][3]};
+                uint32_t X[4];
+                perm_x_for4(xw, X);
+                a = u32x4_t{X[0], X[1], X[2], X[3]};
+            } else {
+                a = st.xa[i];
+            }
+            const bf16x8_t A = as_bf16x8(a);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                uint32_t p[4];
+                if constexpr (BITS == 4) {
+                    unpack4_magic(st.code[t][i], p, kMask, kMagic);
+                } else {
+                    // quad q of k-block 4u+i: words 2*(i&1), 2*(i&1)+1 of register 2t + i/2
+                    const u32x4_t& c = st.code[2 * t + (i >> 1)];
+                    unpack8_pairs(c[2 * (i & 1)], &p[0]);
+                    unpack8_pairs(c[2 * (i & 1) + 1], &p[2]);
+                }
+                D[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(u32x4_t{p[0], p[1], p[2], p[3]}), D[t], 0, 0, 0);
+            }
+            DX = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(ones), DX, 0, 0, 0);
+            // end of a group cycle (or of K): fold the cycle into the totals
+            if (kb < KB && (((kb + 1) >> cl_shift) != (kb >> cl_shift) || kb + 1 == KB)) rescale(kb >> cl_shift);
+        }
+    };
+
+    // one-deep pipeline over k-quads, ping-ponging two stages
+    if (u0 < u1) {
+        St A, B;
+        issue(u0, A);
+        if (u0 + 1 < u1) issue(u0 + 1, B);
+        for (int u = u0; u < u1; u += 2) {
+            if (u > u0 && u + 1 < u1) issue(u + 1, B);
+            compute(u, A);
+            if (u + 1 >= u1) break;
+            if (u + 2 < u1) issue(u + 2, A);
+            compute(u + 1, B);
+        }
+        // a slice that ends mid-cycle has partial sums left in D
+        const int last = min(4 * u1, KB) - 1;
+        if (((last + 1) >> cl_shift) == (last >> cl_shift) && last + 1 != KB) rescale(last >> cl_shift);
+    }
+
+    // combine the waves' partial sums and store
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int i = 0; i < NMT; ++i) red[((wv * T + t) * 64 + lane) * NMT + i] = tot[t][i];
+    __syncthreads();
+    // output (t, m, nl): sum over waves and over the lanes (quarters q, rows j) that hold m
+    for (int o = threadIdx.x; o < T * MT * 16; o += WPB * 64) {
+        const int t = o / (MT * 16), m = (o / 16) % MT, n = o % 16;
+        const int nn = n0 + 16 * t + n;
+        if (m >= M || nn >= N) continue;
+        float v = 0.f;
+        for (int ww = 0; ww < WPB; ++ww) {
+            // rows r with r / GS == m live in quarters q = r / 4
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+#pragma unroll
+                for (int i = 0; i < NMT; ++i) {
+                    const int r = 4 * qq + (NMT == 1 ? 0 : i * GS);
+                    if (r / GS != m) continue;
+                    v += red[((ww * T + t) * 64 + qq * 16 + n) * NMT + i];
+                }
+            }
+        }
+        store_out(y, (int64_t)m * N + nn, y_dtype, v, bias, nn);
+    }
+}
+
+template <int BITS, int SBT, int MT, int T, int WPB>
+hipError_t launch_t(const QmmArgs& a) {
+    constexpr int NMT = MT >= 4 ? MT / 4 : 1;
+    const int blocks = (int)((a.N + 16 * T - 1) / (16 * T));
+    const size_t lds = sizeof(float) * WPB * T * 64 * NMT;
+    const int gs_shift = __builtin_ctz((unsigned)a.group_size);
+    hipLaunchKernelGGL((qmv_mfma_kernel<BITS, SBT, MT, T, WPB>), dim3(blocks), dim3(WPB * 64), lds, a.stream,
+                       (const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y,
+                       a.bias, (int)a.M, (int)a.N, (int)a.K, gs_shift, a.y_dtype);
+    return hipGetLastError();
+}
+
+int pick_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
+
+// tiles per block and waves per block: T=4 amortises the x operand over four
+// 16-row tiles; two tiles when four would leave too few waves in flight, when
+// the cross-wave reduction would need more than 32 KiB of LDS, or (8-bit) when
+// 16 waves per block leave too few registers for four tiles; 16 K-splitting
+// waves once K has at least 16 k-quads, else 4
+void pick_tw(int64_t M, int64_t N, int64_t K, int bits, int* T, int* WPB) {
+    const int64_t KQ = (K / 32 + 3) / 4;
+    const int nmt = M > 4 ? (M > 8 ? 4 : 2) : 1;
+    const int wpb = KQ >= 16 ? 16 : 4;
+    int t = 4;
+    if (((N + 63) / 64) * wpb < 2048 || wpb * 4 * 64 * nmt * 4 > 32768) t = 2;
+    if (bits == 8 && wpb == 16) t = 2;  // 8-bit stages need the registers of two tiles
+    *T = t;
+    *WPB = wpb;
+}
+
+template <int BITS, int SBT, int MT, int T>
+hipError_t launch_w(const QmmArgs& a, int wpb) {
+    return wpb == 16 ? launch_t<BITS, SBT, MT, T, 16>(a) : launch_t<BITS, SBT, MT, T, 4>(a);
+}
+
+template <int BITS, int SBT, int MT>
+hipError_t launch_tt(const QmmArgs& a) {
+    int T, WPB;
+    pick_tw(a.M, a.N, a.K, a.bits, &T, &WPB);
+    return T == 4 ? launch_w<BITS, SBT, MT, 4>(a, WPB) : launch_w<BITS, SBT, MT, 2>(a, WPB);
+}
+
+template <int BITS, int SBT>
+hipError_t launch_mt(const QmmArgs& a) {
+    switch (pick_mt(a.M)) {
+        case 1: return launch_tt<BITS, SBT, 1>(a);
+        case 2: return launch_tt<BITS, SBT, 2>(a);
+        case 4: return launch_tt<BITS, SBT, 4>(a);
+        case 8: return launch_tt<BITS, SBT, 8>(a);
+        default: return launch_tt<BITS, SBT, 16>(a);
+    }
+}
+
+}  // namespace
+
+void qmv_mfma_config(const QmmArgs& a, int* tiles_per_block, int* m_tile, int* waves_per_block) {
+    int T, WPB;
+    pick_tw(a.M, a.N, a.K, a.bits, &T, &WPB);
+    if (tiles_per_block) *tiles_per_block = T;
+    if (m_tile) *m_tile = pick_mt(a.M);
+    if (waves_per_block) *waves_per_block = WPB;
+}
+
+hipError_t launch_qmv_mfma(const QmmArgs& a) {
+    if (a.bits == 4)
+        return a.sb_dtype == DT_F16 ? launch_mt<4, DT_F16>(a) : launch_mt<4, DT_BF16>(a);
+    return a.sb_dtype == DT_F16 ? launch_mt<8, DT_F16>(a) : launch_mt<8, DT_BF16>(a);
+}
+
+}  // namespace miqmm

@@ -88,9 +88,13 @@ def test_other_entry_points_validate(lib):
 def test_query_route(lib):
     import miqmm
 
-    for M in (1, 2, 8, 16):
+    for M in (1, 2):
         route, tiles = miqmm.query_route(M, 14336, 4096, 64, 4)
-        assert route == miqmm.ROUTE_QMV and tiles[0] in (2, 4) and tiles[1] >= M
+        assert route == miqmm.ROUTE_QMV_DOT and tiles[0] in (1, 2, 4) and tiles[1] >= M and tiles[2] in (16, 32, 64)
+    for M in (3, 8, 16):
+        route, tiles = miqmm.query_route(M, 14336, 4096, 64, 4)
+        assert route == miqmm.ROUTE_QMV and tiles[0] in (2, 4) and tiles[1] >= M and tiles[2] in (4, 16)
+    assert miqmm.query_route(1, 151936, 896, 64, 4)[1][2] == 32  # 28 chunks per row -> 32 lanes
     route, tiles = miqmm.query_route(2048, 14336, 4096, 64, 4)
     assert route == miqmm.ROUTE_QMM and tiles[2] == 64
     with pytest.raises(miqmm.MiqmmError) as e:
