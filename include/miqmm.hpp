@@ -64,6 +64,9 @@ inline Dtype result_type(Dtype x, Dtype scales) { return x == scales ? x : Dtype
 inline void quantized_matmul(Array& out, const Array& x, const Array& w, const Array& scales,
                              const Array& biases, bool transpose, int group_size, int bits,
                              void* stream = nullptr, const Array* bias = nullptr) {
+    if (bits != 4 && bits != 8)  // same statuses as the C ABI, before any shape math
+        throw Exception(bits == 2 || bits == 3 || bits == 5 || bits == 6 ? MIQMM_ENOTSUP : MIQMM_EINVAL,
+                        "miqmm: bits must be 4 or 8");
     if (w.shape.size() != 2 || w.dtype != Dtype::uint32)
         throw Exception(MIQMM_EINVAL, "miqmm: w must be a 2-D uint32 array");
     if (x.shape.empty()) throw Exception(MIQMM_EINVAL, "miqmm: x must have at least one dimension");
@@ -86,6 +89,9 @@ inline void quantized_matmul(Array& out, const Array& x, const Array& w, const A
 // out [N, K] = scales * q + biases per group
 inline void dequantize(Array& out, const Array& w, const Array& scales, const Array& biases,
                        int group_size, int bits, void* stream = nullptr) {
+    if (bits != 4 && bits != 8)
+        throw Exception(bits == 2 || bits == 3 || bits == 5 || bits == 6 ? MIQMM_ENOTSUP : MIQMM_EINVAL,
+                        "miqmm: bits must be 4 or 8");
     const int64_t N = w.dim(0), K = w.dim(1) * 32 / bits;
     if (out.size() != N * K) throw Exception(MIQMM_EINVAL, "miqmm: out must be [N, K]");
     check(miqmm_dequantize(out.data, static_cast<const uint32_t*>(w.data), scales.data, biases.data, N, K,

@@ -48,23 +48,29 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, RNE
 }
 
-// store one output element in the requested dtype; `bias` (nullable, dtype of
-// y) is added after the matmul result is rounded, as QuantizedLinear does
-// (quantized_matmul, then + bias as a separate op).
+// one output element rounded to y's 16-bit dtype (fp16 or bf16); `bias`
+// (nullable, dtype of y) is added after the matmul result is rounded, as
+// QuantizedLinear does (quantized_matmul, then + bias as a separate op).
+__device__ __forceinline__ uint16_t out_half_bits(int y_dtype, float v, const void* bias, int64_t bidx) {
+    if (y_dtype == DT_F16) {
+        uint16_t h = f32_to_f16_bits(f32_pinned(v));
+        if (bias)
+            h = f32_to_f16_bits(f32_pinned(f16_bits_to_f32(h) + f16_bits_to_f32(((const uint16_t*)bias)[bidx])));
+        return h;
+    }
+    uint16_t h = f32_to_bf16_bits(v);
+    if (bias) h = f32_to_bf16_bits(bf16_bits_to_f32(h) + bf16_bits_to_f32(((const uint16_t*)bias)[bidx]));
+    return h;
+}
+
+// store one output element in the requested dtype (bias as above)
 __device__ __forceinline__ void store_out(void* y, int64_t idx, int y_dtype, float v,
                                           const void* bias, int64_t bidx) {
     if (y_dtype == DT_F32) {
         if (bias) v += ((const float*)bias)[bidx];
         ((float*)y)[idx] = v;
-    } else if (y_dtype == DT_F16) {
-        uint16_t h = f32_to_f16_bits(f32_pinned(v));
-        if (bias)
-            h = f32_to_f16_bits(f32_pinned(f16_bits_to_f32(h) + f16_bits_to_f32(((const uint16_t*)bias)[bidx])));
-        ((uint16_t*)y)[idx] = h;
     } else {
-        uint16_t h = f32_to_bf16_bits(v);
-        if (bias) h = f32_to_bf16_bits(bf16_bits_to_f32(h) + bf16_bits_to_f32(((const uint16_t*)bias)[bidx]));
-        ((uint16_t*)y)[idx] = h;
+        ((uint16_t*)y)[idx] = out_half_bits(y_dtype, v, bias, bidx);
     }
 }
 

@@ -6,23 +6,42 @@
 // (src/engine/mlx_lm/models/llama.rs:195-197,249,293-294 with x [1, L, K],
 // L up to prefill_chunk; src/engine/mlx_native.rs:1918-1922,2094-2102).
 //
-// Block tile BM x BN x 64 (BM = 2*WM, BN = 2*WN), four waves in a 2x2 grid,
-// each owning a WM x WN sub-tile computed with v_mfma_f32_32x32x16_bf16.  Per
-// 64-wide k-step the block
-//   - copies the x tile [BM, 64] bf16 into LDS unchanged,
-//   - dequantizes the W tile [BN, 64] in fp32 (fma(s, q, b), the reference's
-//     formula) and stores it to LDS as bf16, k-contiguous per output column,
-// while the next k-step's x rows, packed codes, scales and biases are already
-// in flight into registers.  LDS rows are padded to 72 bf16 (144 B) so the
-// 16-byte fragment reads of eight consecutive rows hit disjoint banks.
+// Block tile 256 x BN x 64 with four waves in a 2 x 2 grid; each wave owns a
+// 128 x (BN/2) sub-tile computed with v_mfma_f32_32x32x16_bf16 (the
+// accumulators, up to 256 fp32 per lane, live in AGPRs).  A big wave tile
+// keeps LDS reads per MFMA flop low: each 16-wide k step a wave reads 4 A and
+// BN/64 B fragments of 1 KiB for 4*BN/64 MFMAs.
+//
+// One block per CU, so the pipeline, not other waves, hides memory latency.
+// At k-step t the block
+//   - loads the packed codes, scales and biases of step t+2 into registers,
+//   - copies the x tile of step t+2 straight from HBM into a 3-stage LDS ring
+//     (buffer_load ... lds; no registers, no VALU),
+//   - runs the MFMAs of step t from LDS,
+//   - dequantizes the codes of step t+1 in fp32 (fma(s, q, b), the reference's
+//     formula) and stores them into the other half of a 2-stage LDS buffer
+//     as bf16, k-contiguous per output column,
+// with one barrier per k-step.  LDS: 3 x 32 KiB of x + 2 x BN*128 B of W.
+//
+// LDS layout of a tile [R rows, 64 k] (bf16): four k-slices of 16, each
+// [R rows x 32 B]; within a slice row r holds its two 16-byte halves (k 0-7,
+// 8-15) swapped when bit 3 of r is set.  gfx950's LDS serves sixteen 16-byte
+// lanes per pass (64 banks): a fragment read of 16 consecutive rows covers all
+// 64 banks once, and every fragment address is one per-lane base plus
+// compile-time offsets (slice * R * 32 + tile row * 32), which keeps address
+// registers out of the way of the 256 accumulators.
+//
+// Rounding the dequantized weight to bf16 before the MFMA follows MLX's qmm,
+// which dequantizes W tiles into threadgroup memory in the activation type.
 #include "miqmm_device.h"
 #include "miqmm_internal.h"
 
 namespace miqmm {
 namespace {
 
+constexpr int kBM = 256;
 constexpr int kBK = 64;
-constexpr int kLDK = kBK + 8;
+constexpr int kRowBytes = kBK * 2;  // one LDS row: 64 bf16
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     bf16x2_t v = {(__bf16)lo, (__bf16)hi};
@@ -35,14 +54,10 @@ __device__ __forceinline__ void dequant_chunk4(const u32x4_t& q, float s, float 
     for (int wi = 0; wi < 4; ++wi) {
         const uint32_t lo = q[wi] & 0x0F0F0F0Fu;         // codes 0,2,4,6 of the word
         const uint32_t hi = (q[wi] >> 4) & 0x0F0F0F0Fu;  // codes 1,3,5,7
-        out[wi][0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(lo), b),
-                                 fmaf(s, ubyte_f32<0>(hi), b));
-        out[wi][1] = pack_bf16x2(fmaf(s, ubyte_f32<1>(lo), b),
-                                 fmaf(s, ubyte_f32<1>(hi), b));
-        out[wi][2] = pack_bf16x2(fmaf(s, ubyte_f32<2>(lo), b),
-                                 fmaf(s, ubyte_f32<2>(hi), b));
-        out[wi][3] = pack_bf16x2(fmaf(s, ubyte_f32<3>(lo), b),
-                                 fmaf(s, ubyte_f32<3>(hi), b));
+        out[wi][0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<0>(hi), b));
+        out[wi][1] = pack_bf16x2(fmaf(s, ubyte_f32<1>(lo), b), fmaf(s, ubyte_f32<1>(hi), b));
+        out[wi][2] = pack_bf16x2(fmaf(s, ubyte_f32<2>(lo), b), fmaf(s, ubyte_f32<2>(hi), b));
+        out[wi][3] = pack_bf16x2(fmaf(s, ubyte_f32<3>(lo), b), fmaf(s, ubyte_f32<3>(hi), b));
     }
 }
 
@@ -51,84 +66,127 @@ __device__ __forceinline__ void dequant_chunk8(const u32x4_t& q, float s, float 
 #pragma unroll
     for (int wi = 0; wi < 4; ++wi) {
         const uint32_t v = q[wi];
-        out[wi >> 1][(wi & 1) * 2 + 0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(v), b),
-                                                     fmaf(s, ubyte_f32<1>(v), b));
-        out[wi >> 1][(wi & 1) * 2 + 1] = pack_bf16x2(fmaf(s, ubyte_f32<2>(v), b),
-                                                     fmaf(s, ubyte_f32<3>(v), b));
+        out[wi >> 1][(wi & 1) * 2 + 0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(v), b), fmaf(s, ubyte_f32<1>(v), b));
+        out[wi >> 1][(wi & 1) * 2 + 1] = pack_bf16x2(fmaf(s, ubyte_f32<2>(v), b), fmaf(s, ubyte_f32<3>(v), b));
     }
 }
 
-template <int BITS, int SBT, int WM, int WN>
-__global__ __launch_bounds__(256) void qmm_kernel(const uint16_t* __restrict__ x,
-                                                  const uint32_t* __restrict__ w,
-                                                  const uint16_t* __restrict__ sc,
-                                                  const uint16_t* __restrict__ bi,
-                                                  void* __restrict__ y, const void* __restrict__ bias,
-                                                  int M, int N, int K, int gs_shift, int y_dtype) {
-    constexpr int BM = 2 * WM, BN = 2 * WN;
-    constexpr int TM = WM / 32, TN = WN / 32;
-    constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;       // codes per 16-byte chunk
-    constexpr int CPR = kBK >> CPC_SHIFT;              // code chunks per row per k-step
-    constexpr int A_PER = BM * (kBK / 8) / 256;        // 16-byte x chunks per thread
-    constexpr int W_PER = BN * CPR / 256;              // 16-byte code chunks per thread
-    static_assert(A_PER >= 1 && W_PER >= 1, "tile too small for 256 threads");
+// s_waitcnt immediate for vmcnt(n) lgkmcnt(0) (vmcnt bits 3:0 and 15:14, expcnt 6:4 left at 7)
+constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
 
-    __shared__ __attribute__((aligned(16))) uint16_t sA[BM * kLDK];
-    __shared__ __attribute__((aligned(16))) uint16_t sB[BN * kLDK];
+// byte offset of the 16-byte piece (k-slice kk, half fk) of row r in a tile of R rows
+__device__ __forceinline__ uint32_t lds_off(int R, int r, int kk, int fk) {
+    return kk * R * 32 + r * 32 + ((fk ^ ((r >> 3) & 1)) << 4);
+}
 
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int BITS, int W_PER>
+struct WRegs {
+    u32x4_t q[W_PER];
+    uint16_t s[W_PER], b[W_PER];
+};
+
+template <int BITS, int SBT, int BN>
+__global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict__ x,
+                                                     const uint32_t* __restrict__ w,
+                                                     const uint16_t* __restrict__ sc,
+                                                     const uint16_t* __restrict__ bi,
+                                                     void* __restrict__ y, const void* __restrict__ bias,
+                                                     int M, int N, int K, int gs_shift, int y_dtype) {
+    constexpr int WN = BN / 2;                    // wave tile 128 x WN
+    constexpr int TM = 4, TN = WN / 32;           // 32x32 MFMA tiles per wave
+    constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk
+    constexpr int CPR = kBK >> CPC_SHIFT;         // code chunks per W row per k-step (2 or 4)
+    constexpr int W_PER = BN * CPR / 256;         // code chunks per thread (1, 2 or 4)
+    constexpr int A_STAGE = kBM * kRowBytes;      // 32 KiB
+    constexpr int B_STAGE = BN * kRowBytes;
+    constexpr int B_BASE = 3 * A_STAGE;
+    static_assert(W_PER >= 1 && CPR % W_PER == 0, "code chunks per thread");
+    // vector-memory loads one thread issues per k-step: 8 x copies + codes,
+    // scales and biases of W_PER chunks
+    constexpr int LOADS = 8 + 3 * W_PER;
+    static_assert(LOADS < 64, "vmcnt range");
+
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wid >> 1, wn = wid & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * BN;
     const int KT = (K + kBK - 1) / kBK;
-    const int64_t KW = (int64_t)K * BITS / 32;
+    const uint32_t xrow = (uint32_t)K * 2;
+    const uint32_t wrow = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
+    const int mrows = min(kBM, M - m0), nrows = min(BN, N - n0);
+    const auto xr = make_rsrc(x + (size_t)m0 * K, (uint32_t)mrows * xrow);
+    const auto wr = make_rsrc((const char*)w + (size_t)n0 * wrow, (uint32_t)nrows * wrow);
+    const auto sr = make_rsrc(sc + (size_t)n0 * G, (uint32_t)nrows * G * 2);
+    const auto br = make_rsrc(bi + (size_t)n0 * G, (uint32_t)nrows * G * 2);
 
-    u32x4_t ra[A_PER], rw[W_PER];
-    float rs[W_PER], rb[W_PER];
-
-    auto load_tile = [&](int kt) {
-        const int kb = kt * kBK;
+    // x tile -> LDS: wave `wid` fills k-slice `wid` ([256 rows x 32 B]) with
+    // eight 1 KiB instructions; lane i of an instruction lands at byte 16*i,
+    // i.e. row i/2 of its 32-row group, stored half i%2, so it loads logical
+    // half (i%2) ^ (bit 3 of the row)
+    auto issue_a = [&](int kt) {
+        const int kb = kt * kBK + wid * 16;
+        char* slice = smem + (kt % 3) * A_STAGE + wid * kBM * 32;
 #pragma unroll
-        for (int i = 0; i < A_PER; ++i) {
-            const int idx = tid + 256 * i, row = idx >> 3, ch = idx & 7;
-            const int gm = m0 + row, k = kb + ch * 8;
-            ra[i] = (gm < M && k < K) ? ldg16(x + (int64_t)gm * K + k) : u32x4_t{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int i = 0; i < W_PER; ++i) {
-            const int idx = tid + 256 * i, row = idx / CPR, ch = idx % CPR;
-            const int gn = n0 + row, kc = kb + (ch << CPC_SHIFT);
-            const bool ok = gn < N && kc < K;
-            const int gnc = min(gn, N - 1);
-            rw[i] = ok ? ldg16(w + (int64_t)gn * KW + (kc * BITS) / 32) : u32x4_t{0, 0, 0, 0};
-            const int64_t sidx = (int64_t)gnc * G + (min(kc, K - 1) >> gs_shift);
-            rs[i] = ok ? half_to_f32<SBT>(sc[sidx]) : 0.f;
-            rb[i] = ok ? half_to_f32<SBT>(bi[sidx]) : 0.f;
+        for (int j = 0; j < 8; ++j) {
+            const int row = j * 32 + (lane >> 1);
+            const int fk = (lane & 1) ^ ((row >> 3) & 1);
+            const int k = kb + fk * 8;
+            const uint32_t off = k < K ? (uint32_t)row * xrow + (uint32_t)k * 2 : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(slice + j * 1024), 16, off, 0, 0, 0);
         }
     };
 
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int i = 0; i < A_PER; ++i) {
-            const int idx = tid + 256 * i, row = idx >> 3, ch = idx & 7;
-            *reinterpret_cast<u32x4_t*>(&sA[row * kLDK + ch * 8]) = ra[i];
-        }
+    // this thread's W row and first code chunk
+    const int wrow_t = tid / (CPR / W_PER);
+    const int wch0 = (tid % (CPR / W_PER)) * W_PER;
+    using WR = WRegs<BITS, W_PER>;
+    auto load_w = [&](int kt, WR& r) {
+        const int kb = kt * kBK;
 #pragma unroll
         for (int i = 0; i < W_PER; ++i) {
-            const int idx = tid + 256 * i, row = idx / CPR, ch = idx % CPR;
-            uint16_t* dst = &sB[row * kLDK + (ch << CPC_SHIFT)];
-            if constexpr (BITS == 4) {
-                u32x4_t o[4];
-                dequant_chunk4(rw[i], rs[i], rb[i], o);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4_t*>(dst + j * 8) = o[j];
-            } else {
-                u32x4_t o[2];
-                dequant_chunk8(rw[i], rs[i], rb[i], o);
-#pragma unroll
-                for (int j = 0; j < 2; ++j) *reinterpret_cast<u32x4_t*>(dst + j * 8) = o[j];
-            }
+            const int kc = kb + ((wch0 + i) << CPC_SHIFT);
+            // past the end of K (last step when K % 64 == 32): offsets pushed out of range
+            const uint32_t oob = kc < K ? 0u : kOOB;
+            r.q[i] = bload16(wr, ((uint32_t)wrow_t * wrow + (uint32_t)kc * BITS / 8) | oob);
+            const uint32_t so = (((uint32_t)wrow_t * G + (uint32_t)(kc >> gs_shift)) * 2) | oob;
+            r.s[i] = bload2(sr, so);
+            r.b[i] = bload2(br, so);
         }
+    };
+    // dequantize one 16-byte LDS chunk (8 codes, one W word for 4-bit, two
+    // half-words for 8-bit) of the codes in `r` into B stage kt&1.  Chunk
+    // index e runs over the thread's W_PER*CPC/8 chunks.
+    constexpr int W_CHUNKS = W_PER * (1 << CPC_SHIFT) / 8;  // LDS chunks per thread per k-step
+    auto store_w_chunk = [&](int kt, const WR& r, int e) {
+        char* sB = smem + B_BASE + (kt & 1) * B_STAGE;
+        const int i = e / ((1 << CPC_SHIFT) / 8), j = e % ((1 << CPC_SHIFT) / 8);
+        const float s = half_to_f32<SBT>(r.s[i]), b = half_to_f32<SBT>(r.b[i]);
+        const int c = (((wch0 + i) << CPC_SHIFT) >> 3) + j;
+        u32x4_t o;
+        if constexpr (BITS == 4) {
+            const uint32_t word = r.q[i][j];
+            const uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
+            o[0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<0>(hi), b));
+            o[1] = pack_bf16x2(fmaf(s, ubyte_f32<1>(lo), b), fmaf(s, ubyte_f32<1>(hi), b));
+            o[2] = pack_bf16x2(fmaf(s, ubyte_f32<2>(lo), b), fmaf(s, ubyte_f32<2>(hi), b));
+            o[3] = pack_bf16x2(fmaf(s, ubyte_f32<3>(lo), b), fmaf(s, ubyte_f32<3>(hi), b));
+        } else {
+            const uint32_t w0 = r.q[i][2 * j], w1 = r.q[i][2 * j + 1];
+            o[0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(w0), b), fmaf(s, ubyte_f32<1>(w0), b));
+            o[1] = pack_bf16x2(fmaf(s, ubyte_f32<2>(w0), b), fmaf(s, ubyte_f32<3>(w0), b));
+            o[2] = pack_bf16x2(fmaf(s, ubyte_f32<0>(w1), b), fmaf(s, ubyte_f32<1>(w1), b));
+            o[3] = pack_bf16x2(fmaf(s, ubyte_f32<2>(w1), b), fmaf(s, ubyte_f32<3>(w1), b));
+        }
+        *reinterpret_cast<u32x4_t*>(sB + lds_off(BN, wrow_t, c >> 1, c & 1)) = o;
+    };
+    auto store_w = [&](int kt, const WR& r) {
+#pragma unroll
+        for (int e = 0; e < W_CHUNKS; ++e) store_w_chunk(kt, r, e);
     };
 
     f32x16_t acc[TM][TN];
@@ -139,69 +197,177 @@ __global__ __launch_bounds__(256) void qmm_kernel(const uint16_t* __restrict__ x
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    const int frag_row = lane & 31, frag_k = (lane >> 5) * 8;
-    load_tile(0);
-    for (int kt = 0; kt < KT; ++kt) {
-        store_tile();
-        __syncthreads();
-        if (kt + 1 < KT) load_tile(kt + 1);
+    // fragment of a 32x32x16 MFMA: lane l holds row l%32, k = 8*(l/32) .. +8 of the 16-wide step
+    const int frow = lane & 31, fk = lane >> 5;
+    // per-lane part of a fragment address: row frow of a 32-row tile, half fk
+    const uint32_t fbase = (uint32_t)frow * 32 + ((fk ^ ((frow >> 3) & 1)) << 4);
+    auto read_frags = [&](int kt, int kk, bf16x8_t* af, bf16x8_t* bf) {
+        const char* sA = smem + (kt % 3) * A_STAGE + fbase;
+        const char* sB = smem + B_BASE + (kt & 1) * B_STAGE + fbase;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            af[i] = *reinterpret_cast<const bf16x8_t*>(sA + kk * kBM * 32 + (wm * 128 + i * 32) * 32);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            bf[j] = *reinterpret_cast<const bf16x8_t*>(sB + kk * BN * 32 + (wn * WN + j * 32) * 32);
+    };
+
+    // step t: codes of t+2 into `nxt`, x of t+2 into the ring, MFMAs of t,
+    // dequant of t+1 (held in `cur`) spread over the four 16-wide sub-steps so
+    // its VALU work issues between MFMAs.  The loads are issued on every step,
+    // also past the last one (out-of-range offsets read zeros into a stage
+    // nobody reads again): the compiler's wait counts for `cur` are then the
+    // same on every path.  The end-of-step barrier is a bare s_barrier with
+    // explicit waits, because __syncthreads() would also wait for the x copies
+    // of t+2, which are LDS writes in flight.
+    constexpr int E_PER_KK = (W_CHUNKS + 3) / 4;
+    auto step = [&](int t, const WR& cur, WR& nxt) {
+        load_w(t + 2, nxt);
+        issue_a(t + 2);
+        bf16x8_t af[2][TM], bf[2][TN];
+        read_frags(t, 0, af[0], bf[0]);
 #pragma unroll
         for (int kk = 0; kk < kBK / 16; ++kk) {
-            bf16x8_t af[TM], bf[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-                af[i] = *reinterpret_cast<const bf16x8_t*>(
-                    &sA[(wm * WM + i * 32 + frag_row) * kLDK + kk * 16 + frag_k]);
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                bf[j] = *reinterpret_cast<const bf16x8_t*>(
-                    &sB[(wn * WN + j * 32 + frag_row) * kLDK + kk * 16 + frag_k]);
+            if (kk + 1 < kBK / 16) read_frags(t, kk + 1, af[(kk + 1) & 1], bf[(kk + 1) & 1]);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        __syncthreads();
-    }
-
-    // D of a 32x32 MFMA: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][i], bf[kk & 1][j], acc[i][j], 0,
+                                                                      0, 0);
+            if (t + 1 < KT) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+                for (int e = kk * E_PER_KK; e < (kk + 1) * E_PER_KK && e < W_CHUNKS; ++e) store_w_chunk(t + 1, cur, e);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // x of step t+1 (direct-to-LDS) must have landed while the LOADS of
+        // step t+2 stay in flight (loads retire in order); the LDS writes of
+        // the dequantized W of t+1 must be done before other waves read them
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS));
+        __builtin_amdgcn_s_barrier();
+    };
+
+    WR w0, w1;
+    // same issue order as the loop, unconditionally (past K the offsets are
+    // out of range), so the loop starts with the wait counts it keeps
+    load_w(0, w0);
+    issue_a(0);
+    load_w(1, w1);
+    issue_a(1);
+    store_w(0, w0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS));  // x of step 0 landed
+    __builtin_amdgcn_s_barrier();
+    int t = 0;
+    for (; t + 1 < KT; t += 2) {
+        step(t, w1, w0);
+        step(t + 1, w0, w1);
+    }
+    if (t < KT) step(t, w1, w0);
+    // the prefetches past the last step (out of range, zero-filled) still
+    // write the x ring; they must land before the ring is reused below
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+
+    // Epilogue, one 32-row band at a time: each wave stages its fp32 results
+    // in its own LDS region (the pipeline buffers are free after the last
+    // barrier), then writes runs of 8 columns per lane.  D of a 32x32 MFMA:
+    // lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32.  Rows
+    // are padded to WN+32 floats so the two row groups of one store fall in
+    // different banks.
+    constexpr int ES = WN + 32;
+    float* stage = reinterpret_cast<float*>(smem) + wid * 32 * ES;
+    const int wrow0 = m0 + wm * 128, wcol0 = n0 + wn * WN;
+    const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const int col = n0 + wn * WN + j * 32 + (lane & 31);
-                if (row < M && col < N) store_out(y, (int64_t)row * N + col, y_dtype, acc[i][j][r], bias, col);
+            for (int r = 0; r < 16; ++r)
+                stage[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ES + j * 32 + (lane & 31)] = acc[i][j][r];
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+        __builtin_amdgcn_wave_barrier();
+        constexpr int RUNS = WN / 8;
+#pragma unroll 1
+        for (int p = lane; p < 32 * RUNS; p += 64) {
+            const int row = p / RUNS, c8 = p % RUNS;
+            const int gr = wrow0 + i * 32 + row, gc = wcol0 + c8 * 8;
+            if (gr >= M || gc >= N) continue;
+            const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(stage + row * ES + c8 * 8);
+            const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(stage + row * ES + c8 * 8 + 4);
+            const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            const int64_t o = (int64_t)gr * N + gc;
+            if (vec && y_dtype != DT_F32) {  // gc + 8 <= N since N % 8 == 0
+                u32x4_t h;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    h[e] = (uint32_t)out_half_bits(y_dtype, v[2 * e], bias, gc + 2 * e) |
+                           ((uint32_t)out_half_bits(y_dtype, v[2 * e + 1], bias, gc + 2 * e + 1) << 16);
+                *reinterpret_cast<u32x4_t*>((uint16_t*)y + o) = h;
+            } else if (vec) {
+                f32x4_t a = v0, b = v1;
+                if (bias) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        a[e] += ((const float*)bias)[gc + e];
+                        b[e] += ((const float*)bias)[gc + 4 + e];
+                    }
+                }
+                *reinterpret_cast<f32x4_t*>((float*)y + o) = a;
+                *reinterpret_cast<f32x4_t*>((float*)y + o + 4) = b;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (gc + e < N) store_out(y, o + e, y_dtype, v[e], bias, gc + e);
             }
+        }
+        __builtin_amdgcn_wave_barrier();  // reads of this band before the next band's writes
+    }
 }
 
-constexpr int kWM = 64, kWN = 64;
+template <int BITS, int SBT, int BN>
+hipError_t launch_t(const QmmArgs& a) {
+    constexpr size_t lds = 3 * (size_t)kBM * kRowBytes + 2 * (size_t)BN * kRowBytes;
+    static bool attr_set = false;  // the attribute is per kernel; setting it twice is harmless
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)qmm_kernel<BITS, SBT, BN>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + kBM - 1) / kBM));
+    const int gs_shift = __builtin_ctz((unsigned)a.group_size);
+    hipLaunchKernelGGL((qmm_kernel<BITS, SBT, BN>), grid, dim3(256), lds, a.stream, (const uint16_t*)a.x, a.w,
+                       (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y, a.bias, (int)a.M, (int)a.N,
+                       (int)a.K, gs_shift, a.y_dtype);
+    return hipGetLastError();
+}
+
+// 256-wide tiles unless that leaves fewer tiles than CUs while 128-wide would not
+int pick_bn(int64_t M, int64_t N) {
+    const int64_t mt = (M + kBM - 1) / kBM;
+    const int64_t t256 = mt * ((N + 255) / 256), t128 = mt * ((N + 127) / 128);
+    if (t256 >= 256) return 256;
+    return t128 > t256 ? 128 : 256;
+}
 
 template <int BITS, int SBT>
-hipError_t launch_t(const QmmArgs& a) {
-    const dim3 grid((unsigned)((a.N + 2 * kWN - 1) / (2 * kWN)), (unsigned)((a.M + 2 * kWM - 1) / (2 * kWM)));
-    const int gs_shift = __builtin_ctz((unsigned)a.group_size);
-    hipLaunchKernelGGL((qmm_kernel<BITS, SBT, kWM, kWN>), grid, dim3(256), 0, a.stream,
-                       (const uint16_t*)a.x, a.w, (const uint16_t*)a.scales,
-                       (const uint16_t*)a.biases, a.y, a.bias, (int)a.M, (int)a.N, (int)a.K,
-                       gs_shift, a.y_dtype);
-    return hipGetLastError();
+hipError_t launch_bn(const QmmArgs& a) {
+    return pick_bn(a.M, a.N) == 256 ? launch_t<BITS, SBT, 256>(a) : launch_t<BITS, SBT, 128>(a);
 }
 
 }  // namespace
 
-void qmm_config(const QmmArgs&, int* bm, int* bn, int* bk) {
-    if (bm) *bm = 2 * kWM;
-    if (bn) *bn = 2 * kWN;
+void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk) {
+    if (bm) *bm = kBM;
+    if (bn) *bn = pick_bn(a.M, a.N);
     if (bk) *bk = kBK;
 }
 
 hipError_t launch_qmm(const QmmArgs& a) {
-    if (a.bits == 4) return a.sb_dtype == DT_F16 ? launch_t<4, DT_F16>(a) : launch_t<4, DT_BF16>(a);
-    return a.sb_dtype == DT_F16 ? launch_t<8, DT_F16>(a) : launch_t<8, DT_BF16>(a);
+    if (a.bits == 4) return a.sb_dtype == DT_F16 ? launch_bn<4, DT_F16>(a) : launch_bn<4, DT_BF16>(a);
+    return a.sb_dtype == DT_F16 ? launch_bn<8, DT_F16>(a) : launch_bn<8, DT_BF16>(a);
 }
 
 }  // namespace miqmm
