@@ -150,7 +150,7 @@ def dense_bf16_tflops(torch, M, N, K, iters):
     return 2.0 * M * N * K / t / 1e12
 
 
-def cpu_baseline(miqmm, torch, projs, budget_s=12.0):
+def cpu_baseline(miqmm, torch, projs, budget_s=15.0):
     """the C oracle's fp32 path (OpenMP over N) on the host cores, on the same
     decode step (one replica), repeated until ~budget_s of CPU time"""
     import numpy as np
@@ -174,7 +174,7 @@ def cpu_baseline(miqmm, torch, projs, budget_s=12.0):
             O.c_qmm_f32(x, w, s, b, 1, N, K, 64, 4, nthreads=threads)
         steps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or steps >= 50:
+        if el >= budget_s:
             break
     return {"value": round(step_bytes * steps / el / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
@@ -182,6 +182,49 @@ def cpu_baseline(miqmm, torch, projs, budget_s=12.0):
                       f"C oracle fp32 path (oracle/miqmm_oracle.c, gcc -O3 -fopenmp), {threads} threads, "
                       f"{el:.1f} s; MLX's CPU backend is not available offline",
             "ms_per_step": round(el / steps * 1e3, 3)}
+
+
+PROFILE_DIR = os.path.join(ROOT, "profiles")
+ROOFLINE_PROFILE = os.path.join(PROFILE_DIR, "qmv_lm_head_151936x896_m1.md")
+
+
+def measured_traffic(path=ROOFLINE_PROFILE):
+    """HBM bytes per launch of the roofline kernel from its committed rocprofv3
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), or None"""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def profile_section(miqmm, torch, target):
+    """one measured section alone, so a rocprofv3 run of this command holds only
+    its kernel: the roofline launches, the qmv or qmm headline, or a plain
+    512 MiB device copy (the FETCH_SIZE / WRITE_SIZE calibration)"""
+    if target == "roofline":
+        avg, nb = kernel_roofline(miqmm, torch, LM_HEAD[1], LM_HEAD[2], 1, replicas=8,
+                                  launches_per_graph=64, reps=8)
+        return {"section": target, "shape": "M=1 N=151936 K=896", "timed_launches": 512,
+                "avg_launch_us": round(avg * 1e6, 3), "bytes_per_launch": nb, "GB/s": round(nb / avg / 1e9, 1)}
+    if target == "qmv":
+        avg, nb = kernel_roofline(miqmm, torch, 14336, 4096, 1, replicas=24, launches_per_graph=96, reps=6)
+        return {"section": target, "shape": "M=1 N=14336 K=4096", "timed_launches": 576,
+                "avg_launch_us": round(avg * 1e6, 3), "bytes_per_launch": nb, "GB/s": round(nb / avg / 1e9, 1)}
+    if target == "qmm":
+        tf, tsec = qmm_tflops(miqmm, torch, 2048, 14336, 4096, iters=10)
+        return {"section": target, "shape": "M=2048 N=14336 K=4096", "timed_launches": 10,
+                "avg_launch_us": round(tsec * 1e6, 2), "TFLOP/s": round(tf, 1)}
+    n = 512 << 20
+    a = torch.empty(n // 4, dtype=torch.int32, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(4):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return {"section": target, "bytes_read_per_launch": n, "bytes_written_per_launch": n, "launches": 4}
 
 
 def main():
@@ -192,6 +235,8 @@ def main():
     ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-headline", action="store_true")
+    ap.add_argument("--profile-target", choices=["roofline", "qmv", "qmm", "copy"], default=None,
+                    help="run only this measured section and print its figures (for rocprofv3 summaries)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the quantized-matmul path has no multi-GPU leg here "
@@ -207,6 +252,9 @@ def main():
         sys.exit(2)
     miqmm.lib()
     torch.cuda.set_device(0)
+    if args.profile_target:
+        print(json.dumps(profile_section(miqmm, torch, args.profile_target)), flush=True)
+        return
 
     shapes = step_shapes()
     step_bytes = sum(qbytes(1, N, K) for _, N, K in shapes)
@@ -235,9 +283,9 @@ def main():
                                "lm_head 896->151936; M=1, 4-bit, group 64, bf16 x/scales/biases/y",
                    "launches_per_step": len(shapes), "bytes_per_step": step_bytes,
                    "weight_replicas": args.replicas, "hip_graph": True},
-        "roofline": {"kernel": "qmv lm_head 896->151936 M=1 (qmv_kernel<4,bf16,M1,RPS4>)", "bound": "hbm",
+        "roofline": {"kernel": "qmv lm_head 896->151936 M=1 (qmv_kernel<4, 0, 1, 32, 4>: 4-bit, bf16 scales, 1 row, 32 lanes per row, 4 rows per stage)", "bound": "hbm",
                      "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "avg_launch_us": round(lm_avg * 1e6, 3), "bytes_per_launch": lm_bytes},
     }
     print(f"# step {ms_per_step * 1e3:.1f} us, {gbs:.1f} GB/s; lm_head {lm_avg * 1e6:.2f} us {lm_gbs:.1f} GB/s",
