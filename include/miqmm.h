@@ -47,13 +47,15 @@ typedef enum {
 typedef enum { MIQMM_DT_BF16 = 0, MIQMM_DT_F16 = 1, MIQMM_DT_F32 = 2 } miqmm_dtype;
 
 /* QMV: small-M GEMV on MFMA with exact integer codes; QMM: large-M tiled MFMA
- * with bf16-dequantized W tiles; QMV_DOT: small-M GEMV on v_dot2 (no MFMA),
- * kept as a selectable alternative to QMV. */
+ * with bf16-dequantized W tiles; QMV_DOT: small-M GEMV on v_dot2 (no MFMA);
+ * QMVX: small-M GEMV on MFMA with x staged in LDS (M <= 4 per pass, needs
+ * K/group_size even and min(M,4)*K <= 32768). */
 typedef enum {
     MIQMM_ROUTE_AUTO = 0,
     MIQMM_ROUTE_QMV = 1,
     MIQMM_ROUTE_QMM = 2,
-    MIQMM_ROUTE_QMV_DOT = 3
+    MIQMM_ROUTE_QMV_DOT = 3,
+    MIQMM_ROUTE_QMVX = 4
 } miqmm_route;
 
 /*
@@ -62,8 +64,9 @@ typedef enum {
  * (reached at src/engine/mlx_lm/utils/mod.rs:70-78 and from every
  * QuantizedLinear::forward).  transpose must be 1; bits in {4, 8};
  * group_size in {32, 64, 128}; K % group_size == 0; x and w 16-byte aligned.
- * M == 0 is a no-op.  Route: M <= 2 -> qmv_dot, M <= 16 -> qmv (both HBM-bound
- * GEMVs), else qmm (MFMA-bound tiled matmul).
+ * M == 0 is a no-op.  Route (HBM-bound GEMVs for M <= 16): M == 1 -> qmv_dot,
+ * or qmvx for N >= 65536 with K <= 2048; 2 <= M <= 4 -> qmvx where supported,
+ * else qmv_dot; M <= 16 -> qmv; else qmm (MFMA-bound tiled matmul).
  */
 int miqmm_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
                            const void* biases, int64_t M, int64_t N, int64_t K, int transpose,

@@ -58,10 +58,20 @@ int check_launch(hipError_t e, const char* what) {
     return ok();
 }
 
-// M <= 2: the v_dot2 GEMV streams fastest; 3 <= M <= 16: the MFMA GEMV, whose
-// cost barely grows with M; larger M: the tiled MFMA matmul
-int auto_route(int64_t M) {
-    return M <= 2 ? MIQMM_ROUTE_QMV_DOT : M <= 16 ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
+// Measured on MI355X (4-bit g64, cold weights):
+//   M = 1: the v_dot2 GEMV, except for many-row, short-K heads (lm_head 896 ->
+//          151936: 18.8 us against 22.8 us), where the LDS-staged MFMA GEMV wins;
+//   2 <= M <= 4: the LDS-staged MFMA GEMV (14336 x 4096: 12.8 / 16.0 us at
+//          M = 2 / 4 against 15.1 / 22.2 us for v_dot2) when it supports the shape;
+//   5 <= M <= 16: the group-diagonal MFMA GEMV, whose cost barely grows with M;
+//   larger M: the tiled MFMA matmul.
+int auto_route(int64_t M, int64_t N, int64_t K, int group_size) {
+    if (M == 1) {
+        const bool wide_head = N >= 65536 && K <= 2048 && miqmm::qmvx_supported(M, K, group_size);
+        return wide_head ? MIQMM_ROUTE_QMVX : MIQMM_ROUTE_QMV_DOT;
+    }
+    if (M <= 4) return miqmm::qmvx_supported(M, K, group_size) ? MIQMM_ROUTE_QMVX : MIQMM_ROUTE_QMV_DOT;
+    return M <= 16 ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
 }
 
 int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
@@ -76,8 +86,10 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
     if (y_dtype != MIQMM_DT_BF16 && y_dtype != MIQMM_DT_F16 && y_dtype != MIQMM_DT_F32)
         return fail(MIQMM_EINVAL, "y dtype %d invalid", y_dtype);
     if (route != MIQMM_ROUTE_AUTO && route != MIQMM_ROUTE_QMV && route != MIQMM_ROUTE_QMM &&
-        route != MIQMM_ROUTE_QMV_DOT)
+        route != MIQMM_ROUTE_QMV_DOT && route != MIQMM_ROUTE_QMVX)
         return fail(MIQMM_EINVAL, "route %d invalid", route);
+    if (route == MIQMM_ROUTE_QMVX && !miqmm::qmvx_supported(M < 4 ? M : 4, K, group_size))
+        return fail(MIQMM_ENOTSUP, "route qmvx needs K/group_size even and min(M,4)*K <= 32768");
     if (M == 0) return ok();
     if (!y || !x || !w || !scales || !biases) return fail(MIQMM_EINVAL, "null pointer argument");
     if (!aligned16(x) || !aligned16(w))
@@ -87,18 +99,20 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
 
     miqmm::QmmArgs a{y, x, w, scales, biases, bias, M, N, K, group_size, bits, x_dtype, sb_dtype, y_dtype,
                      reinterpret_cast<hipStream_t>(stream)};
-    if (route == MIQMM_ROUTE_AUTO) route = auto_route(M);
-    if (route == MIQMM_ROUTE_QMV || route == MIQMM_ROUTE_QMV_DOT) {
-        // the GEMV kernels handle at most 16 rows of x per pass over W
-        for (int64_t m0 = 0; m0 < M; m0 += 16) {
+    if (route == MIQMM_ROUTE_AUTO) route = auto_route(M, N, K, group_size);
+    if (route == MIQMM_ROUTE_QMV || route == MIQMM_ROUTE_QMV_DOT || route == MIQMM_ROUTE_QMVX) {
+        // the GEMV kernels handle at most 16 (qmvx: 4) rows of x per pass over W
+        const int64_t step = route == MIQMM_ROUTE_QMVX ? 4 : 16;
+        for (int64_t m0 = 0; m0 < M; m0 += step) {
             miqmm::QmmArgs part = a;
-            const int64_t mm = M - m0 < 16 ? M - m0 : 16;
+            const int64_t mm = M - m0 < step ? M - m0 : step;
             part.M = mm;
             part.x = static_cast<const uint16_t*>(x) + m0 * K;
             const int ysz = y_dtype == MIQMM_DT_F32 ? 4 : 2;
             part.y = static_cast<char*>(y) + m0 * N * ysz;
-            st = route == MIQMM_ROUTE_QMV ? check_launch(miqmm::launch_qmv_mfma(part), "qmv launch")
-                                          : check_launch(miqmm::launch_qmv(part), "qmv_dot launch");
+            st = route == MIQMM_ROUTE_QMV    ? check_launch(miqmm::launch_qmv_mfma(part), "qmv launch")
+                 : route == MIQMM_ROUTE_QMVX ? check_launch(miqmm::launch_qmvx(part), "qmvx launch")
+                                             : check_launch(miqmm::launch_qmv(part), "qmv_dot launch");
             if (st != MIQMM_OK) return st;
         }
         return ok();
@@ -166,11 +180,12 @@ int miqmm_query_route(int64_t M, int64_t N, int64_t K, int group_size, int bits,
     a.K = K;
     a.group_size = group_size;
     a.bits = bits;
-    const int route = auto_route(M);
+    const int route = M == 0 ? MIQMM_ROUTE_QMV_DOT : auto_route(M, N, K, group_size);
     if (route_out) *route_out = route;
     if (tile_out) {
         tile_out[0] = tile_out[1] = tile_out[2] = tile_out[3] = 0;
         if (route == MIQMM_ROUTE_QMV) miqmm::qmv_mfma_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
+        else if (route == MIQMM_ROUTE_QMVX) miqmm::qmvx_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
         else if (route == MIQMM_ROUTE_QMV_DOT) miqmm::qmv_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
         else miqmm::qmm_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
     }

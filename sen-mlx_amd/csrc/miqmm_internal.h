@@ -23,11 +23,14 @@ struct QmmArgs {
 hipError_t launch_qmv(const QmmArgs& a);       // VALU dot2 GEMV
 hipError_t launch_qmv_mfma(const QmmArgs& a);  // group-diagonal MFMA GEMV
 hipError_t launch_qmm(const QmmArgs& a);
+hipError_t launch_qmvx(const QmmArgs& a);      // MFMA GEMV, M <= 4, x in LDS
+bool qmvx_supported(int64_t M, int64_t K, int group_size);
 
 // tiling used for a given problem; for reporting
 void qmv_config(const QmmArgs& a, int* rows_per_subgroup, int* m_tile, int* lanes_per_row);
 void qmv_mfma_config(const QmmArgs& a, int* tiles_per_block, int* m_tile, int* waves_per_block);
 void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk);
+void qmvx_config(const QmmArgs& a, int* m_tile, int* k_splits, int* stage_codes);
 
 hipError_t launch_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
                              int64_t N, int64_t K, int group_size, int bits, int sb_dtype,

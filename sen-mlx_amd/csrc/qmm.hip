@@ -74,6 +74,18 @@ __device__ __forceinline__ void dequant_chunk8(const u32x4_t& q, float s, float 
 // s_waitcnt immediate for vmcnt(n) lgkmcnt(0) (vmcnt bits 3:0 and 15:14, expcnt 6:4 left at 7)
 constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
 
+// s_waitcnt with the given immediate, then s_barrier, fenced against compiler
+// reordering of memory operations (the barrier builtin alone is not a memory
+// barrier for the compiler; __syncthreads() would add a release fence that
+// waits for the x copies still in flight)
+#define MIQMM_WAIT_BARRIER(imm)                   \
+    do {                                          \
+        asm volatile("" ::: "memory");            \
+        __builtin_amdgcn_s_waitcnt(imm);          \
+        __builtin_amdgcn_s_barrier();             \
+        asm volatile("" ::: "memory");            \
+    } while (0)
+
 // byte offset of the 16-byte piece (k-slice kk, half fk) of row r in a tile of R rows
 __device__ __forceinline__ uint32_t lds_off(int R, int r, int kk, int fk) {
     return kk * R * 32 + r * 32 + ((fk ^ ((r >> 3) & 1)) << 4);
@@ -244,8 +256,7 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
         // x of step t+1 (direct-to-LDS) must have landed while the LOADS of
         // step t+2 stay in flight (loads retire in order); the LDS writes of
         // the dequantized W of t+1 must be done before other waves read them
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS));
-        __builtin_amdgcn_s_barrier();
+        MIQMM_WAIT_BARRIER(waitcnt_vm_lgkm0(LOADS));
     };
 
     WR w0, w1;
@@ -256,8 +267,7 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     load_w(1, w1);
     issue_a(1);
     store_w(0, w0);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS));  // x of step 0 landed
-    __builtin_amdgcn_s_barrier();
+    MIQMM_WAIT_BARRIER(waitcnt_vm_lgkm0(LOADS));  // x of step 0 landed
     int t = 0;
     for (; t + 1 < KT; t += 2) {
         step(t, w1, w0);
@@ -266,8 +276,7 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     if (t < KT) step(t, w1, w0);
     // the prefetches past the last step (out of range, zero-filled) still
     // write the x ring; they must land before the ring is reused below
-    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
+    MIQMM_WAIT_BARRIER(0x0070);  // vmcnt(0) lgkmcnt(0)
 
     // Epilogue, one 32-row band at a time: each wave stages its fp32 results
     // in its own LDS region (the pipeline buffers are free after the last

@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint16_t* __restrict__ x
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t row = (uint32_t)(sg * R + r);
-            st.q[r] = bload16(wr, cv ? row * row_bytes + (uint32_t)c * 16 : kOOB);
+            st.q[r] = bload16_nt(wr, cv ? row * row_bytes + (uint32_t)c * 16 : kOOB);  // streamed once
             st.s[r] = bload2(sr, (row * G + g) * 2);
             st.b[r] = bload2(br, (row * G + g) * 2);
         }

@@ -120,22 +120,26 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
     }
     DX = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+    // k-quad u of this wave's range into a stage; u >= u1 (the pipeline runs
+    // up to two k-quads past the range) reads zeros.  Codes are streamed once,
+    // so they are loaded non-temporal.
     auto issue = [&](int u, St& st) {
+        const int kbe = u < u1 ? KB : 0;  // k-blocks below kbe are live
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const uint32_t row = (uint32_t)(16 * t + nl);
             if constexpr (BITS == 4) {
                 const int chunk = 4 * u + q;
-                st.code[t] = bload16(wr, chunk < KB ? row * row_bytes + (uint32_t)chunk * 16 : kOOB);
+                st.code[t] = bload16_nt(wr, chunk < kbe ? row * row_bytes + (uint32_t)chunk * 16 : kOOB);
             } else {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     // two k-blocks per 16-byte register: quads of k-blocks 4u+2h, 4u+2h+1
                     const int kb0 = 4 * u + 2 * h;
-                    const uint32_t o0 = kb0 < KB ? row * row_bytes + (uint32_t)kb0 * 32 + q * 8 : kOOB;
-                    const uint32_t o1 = kb0 + 1 < KB ? row * row_bytes + (uint32_t)(kb0 + 1) * 32 + q * 8 : kOOB;
-                    const auto lo = __builtin_amdgcn_raw_buffer_load_b64(wr, o0, 0, 0);
-                    const auto hi = __builtin_amdgcn_raw_buffer_load_b64(wr, o1, 0, 0);
+                    const uint32_t o0 = kb0 < kbe ? row * row_bytes + (uint32_t)kb0 * 32 + q * 8 : kOOB;
+                    const uint32_t o1 = kb0 + 1 < kbe ? row * row_bytes + (uint32_t)(kb0 + 1) * 32 + q * 8 : kOOB;
+                    const auto lo = __builtin_amdgcn_raw_buffer_load_b64(wr, o0, 0, kNonTemporal);
+                    const auto hi = __builtin_amdgcn_raw_buffer_load_b64(wr, o1, 0, kNonTemporal);
                     st.code[2 * t + h] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
                 }
             }
@@ -144,7 +148,7 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
         for (int i = 0; i < 4; ++i) {
             const int kb = 4 * u + i;
             const int gidx = kb >> (gs_shift - 5);
-            const bool live = kb < KB && m_a < M && (gidx % GS) == slot_a;
+            const bool live = kb < kbe && m_a < M && (gidx % GS) == slot_a;
             st.xa[i] = bload16(xr, live ? (uint32_t)m_a * K * 2 + (uint32_t)(kb * 32 + 8 * q) * 2 : kOOB);
         }
     };
@@ -208,18 +212,22 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
         }
     };
 
-    // one-deep pipeline over k-quads, ping-ponging two stages
+    // one-deep pipeline over k-quads, ping-ponging two stages.  Each stage is
+    // refilled right after it is computed, unconditionally: a conditional
+    // issue makes the compiler's wait before each compute count from the path
+    // without the loads, i.e. wait for the stage just issued.
     if (u0 < u1) {
         St A, B;
         issue(u0, A);
-        if (u0 + 1 < u1) issue(u0 + 1, B);
-        for (int u = u0; u < u1; u += 2) {
-            if (u > u0 && u + 1 < u1) issue(u + 1, B);
+        issue(u0 + 1, B);
+        int u = u0;
+        for (; u + 2 <= u1; u += 2) {
             compute(u, A);
-            if (u + 1 >= u1) break;
-            if (u + 2 < u1) issue(u + 2, A);
+            issue(u + 2, A);
             compute(u + 1, B);
+            issue(u + 3, B);
         }
+        if (u < u1) compute(u, A);
         // a slice that ends mid-cycle has partial sums left in D
         const int last = min(4 * u1, KB) - 1;
         if (((last + 1) >> cl_shift) == (last >> cl_shift) && last + 1 != KB) rescale(last >> cl_shift);

@@ -29,13 +29,13 @@ import torch
 __all__ = [
     "MiqmmError", "quantized_matmul", "quantized_linear", "QuantizedLinear", "dequantize",
     "unpack", "synth_problem", "query_route", "result_type", "lib", "LIB_PATH",
-    "OK", "EINVAL", "ENOTSUP", "EHIP", "ROUTE_AUTO", "ROUTE_QMV", "ROUTE_QMM", "ROUTE_QMV_DOT",
+    "OK", "EINVAL", "ENOTSUP", "EHIP", "ROUTE_AUTO", "ROUTE_QMV", "ROUTE_QMM", "ROUTE_QMV_DOT", "ROUTE_QMVX",
 ]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmiqmm.so")
 
 OK, EINVAL, ENOTSUP, EHIP = 0, 1, 2, 3
-ROUTE_AUTO, ROUTE_QMV, ROUTE_QMM, ROUTE_QMV_DOT = 0, 1, 2, 3
+ROUTE_AUTO, ROUTE_QMV, ROUTE_QMM, ROUTE_QMV_DOT, ROUTE_QMVX = 0, 1, 2, 3, 4
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 
 _DT = {torch.bfloat16: DT_BF16, torch.float16: DT_F16, torch.float32: DT_F32}

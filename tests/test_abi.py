@@ -88,13 +88,20 @@ def test_other_entry_points_validate(lib):
 def test_query_route(lib):
     import miqmm
 
-    for M in (1, 2):
+    route, tiles = miqmm.query_route(1, 14336, 4096, 64, 4)
+    assert route == miqmm.ROUTE_QMV_DOT and tiles[0] in (1, 2, 4) and tiles[1] >= 1 and tiles[2] in (16, 32, 64)
+    assert miqmm.query_route(1, 4864, 896, 64, 4)[1][2] == 32  # 28 chunks per row -> 32 lanes
+    # wide, short-K head at M = 1 and 2 <= M <= 4: the LDS-staged MFMA GEMV (m tile, k-splits, codes per stage)
+    route, tiles = miqmm.query_route(1, 151936, 896, 64, 4)
+    assert route == miqmm.ROUTE_QMVX and tiles[:3] == (1, 1, 1024)
+    for M, mt in ((2, 2), (3, 4), (4, 4)):
         route, tiles = miqmm.query_route(M, 14336, 4096, 64, 4)
-        assert route == miqmm.ROUTE_QMV_DOT and tiles[0] in (1, 2, 4) and tiles[1] >= M and tiles[2] in (16, 32, 64)
-    for M in (3, 8, 16):
+        assert route == miqmm.ROUTE_QMVX and tiles[0] == mt and tiles[1] in (1, 2, 4)
+    # qmvx needs an even number of groups per row: K = 96, g = 32 falls back to v_dot2
+    assert miqmm.query_route(2, 128, 96, 32, 4)[0] == miqmm.ROUTE_QMV_DOT
+    for M in (5, 8, 16):
         route, tiles = miqmm.query_route(M, 14336, 4096, 64, 4)
         assert route == miqmm.ROUTE_QMV and tiles[0] in (2, 4) and tiles[1] >= M and tiles[2] in (4, 16)
-    assert miqmm.query_route(1, 151936, 896, 64, 4)[1][2] == 32  # 28 chunks per row -> 32 lanes
     route, tiles = miqmm.query_route(2048, 14336, 4096, 64, 4)
     assert route == miqmm.ROUTE_QMM and tiles[2] == 64
     with pytest.raises(miqmm.MiqmmError) as e:
