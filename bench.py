@@ -283,7 +283,7 @@ def main():
                                "lm_head 896->151936; M=1, 4-bit, group 64, bf16 x/scales/biases/y",
                    "launches_per_step": len(shapes), "bytes_per_step": step_bytes,
                    "weight_replicas": args.replicas, "hip_graph": True},
-        "roofline": {"kernel": "qmv lm_head 896->151936 M=1 (qmv_kernel<4, 0, 1, 32, 4>: 4-bit, bf16 scales, 1 row, 32 lanes per row, 4 rows per stage)", "bound": "hbm",
+        "roofline": {"kernel": "lm_head 896->151936 M=1 (qmvx_kernel<4, 0, 1, 6>: 4-bit, bf16 scales, 1 row of x, group 64)", "bound": "hbm",
                      "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "avg_launch_us": round(lm_avg * 1e6, 3), "bytes_per_launch": lm_bytes},
