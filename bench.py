@@ -5,12 +5,15 @@
 Workload (one "step"): the linear layers of one Qwen2.5-0.5B decode step at
 M=1, 4-bit group-64 affine weights with bf16 scales/biases:
 24 layers x {q 896->896, k 896->128, v 896->128, o 896->896, gate 896->4864,
-up 896->4864, down 4864->896} + lm_head 896->151936 = 169 quantized_matmul
-calls, 279,258,624 algorithmic bytes.  Weights are random (seeded, generated
-on the device); each projection has its own pre-generated x ~ N(0,1).  The
-169 launches of a step are captured once per weight replica into a HIP graph
-and replayed; three replicas (838 MB) rotate so consecutive steps never find
-their weights in the 256 MB Infinity Cache.
+up 896->4864, down 4864->896} + lm_head 896->151936.  Weights are random
+(seeded, generated on the device); x ~ N(0,1) is drawn per layer input, as in
+the model: q, k and v read the attention input, gate and up the MLP input,
+o and down their own.  The step runs q/k/v and gate/up as one grouped call
+each (miqmm_quantized_matmul_grouped), 97 launches; the same step with one
+launch per projection (169 launches) is reported beside it.  The launches of
+a step are captured once per weight replica into a HIP graph and replayed;
+three replicas (838 MB) rotate so consecutive steps never find their weights
+in the 256 MB Infinity Cache.
 
 Printed: one JSON line with the step throughput (value, GB/s), the roofline
 of the dominant kernel (the lm_head GEMV, 76.9 MB per launch), headline
@@ -43,6 +46,11 @@ def qbytes(M, N, K, bits=4, g=64, sb=2, xb=2, yb=2):
     return N * K * bits // 8 + 2 * N * (K // g) * sb + M * K * xb + M * N * yb
 
 
+def group_bytes(Ns, K, M=1):
+    """a grouped call reads x once: the projections' bytes minus the repeated x"""
+    return sum(qbytes(M, N, K) for N in Ns) - (len(Ns) - 1) * M * K * 2
+
+
 def step_shapes():
     shapes = []
     for layer in range(QWEN05_LAYERS):
@@ -64,12 +72,39 @@ def make_replica(miqmm, torch, replica, shapes):
         p.x, p.w, p.s, p.b = miqmm.synth_problem(1, N, K, 64, 4, seed=replica, stream_id=i)
         p.y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
         projs.append(p)
+    # one x per layer input: k and v read q's input, up reads gate's
+    for layer in range(QWEN05_LAYERS):
+        q, k, v, o, gate, up, down = projs[layer * 7:layer * 7 + 7]
+        k.x = v.x = q.x
+        up.x = gate.x
     return projs
 
 
 def run_step(miqmm, projs):
+    """one launch per projection (169)"""
     for p in projs:
         miqmm.quantized_matmul(p.x, p.w, p.s, p.b, True, 64, 4, out=p.y)
+
+
+def run_step_grouped(miqmm, projs):
+    """q/k/v and gate/up as one grouped call each (97 launches)"""
+    for layer in range(QWEN05_LAYERS):
+        q, k, v, o, gate, up, down = projs[layer * 7:layer * 7 + 7]
+        for grp in ((q, k, v), (o,), (gate, up), (down,)):
+            if len(grp) == 1:
+                p = grp[0]
+                miqmm.quantized_matmul(p.x, p.w, p.s, p.b, True, 64, 4, out=p.y)
+            else:
+                miqmm.quantized_matmul_grouped([p.x for p in grp], [p.w for p in grp], [p.s for p in grp],
+                                               [p.b for p in grp], 64, 4, outs=[p.y for p in grp])
+    p = projs[-1]
+    miqmm.quantized_matmul(p.x, p.w, p.s, p.b, True, 64, 4, out=p.y)
+
+
+def step_bytes_grouped():
+    per_layer = group_bytes([896, 128, 128], 896) + qbytes(1, 896, 896) + group_bytes([4864, 4864], 896) + \
+        qbytes(1, 896, 4864)
+    return QWEN05_LAYERS * per_layer + qbytes(1, LM_HEAD[1], LM_HEAD[2])
 
 
 def capture(torch, fn):
@@ -257,17 +292,25 @@ def main():
         return
 
     shapes = step_shapes()
-    step_bytes = sum(qbytes(1, N, K) for _, N, K in shapes)
+    step_bytes = step_bytes_grouped()
+    step_bytes_single = sum(qbytes(1, N, K) for _, N, K in shapes)
     replicas = [make_replica(miqmm, torch, r, shapes) for r in range(args.replicas)]
     for projs in replicas:  # eager warm-up (loads the code objects before capture)
         run_step(miqmm, projs)
+        run_step_grouped(miqmm, projs)
     torch.cuda.synchronize()
-    graphs = [capture(torch, (lambda p=projs: run_step(miqmm, p))) for projs in replicas]
+    graphs = [capture(torch, (lambda p=projs: run_step_grouped(miqmm, p))) for projs in replicas]
     time_graphs(torch, graphs, max(args.warmup, 1))
-    print(f"# timing {args.steps} decode steps ({len(shapes)} launches each)", file=sys.stderr, flush=True)
+    print(f"# timing {args.steps} decode steps (97 launches each)", file=sys.stderr, flush=True)
     t = time_graphs(torch, graphs, args.steps)
     gbs = step_bytes * args.steps / t / 1e9
     ms_per_step = t / args.steps * 1e3
+    del graphs
+    graphs = [capture(torch, (lambda p=projs: run_step(miqmm, p))) for projs in replicas]
+    time_graphs(torch, graphs, max(args.warmup, 1))
+    t1 = time_graphs(torch, graphs, args.steps)
+    single = {"us_per_step": round(t1 / args.steps * 1e6, 2), "launches": len(shapes),
+              "GB/s": round(step_bytes_single * args.steps / t1 / 1e9, 2), "bytes_per_step": step_bytes_single}
 
     # dominant kernel of the step: the lm_head GEMV (N=151936, K=896)
     lm_avg, lm_bytes = kernel_roofline(miqmm, torch, LM_HEAD[1], LM_HEAD[2], 1, replicas=8,
@@ -280,15 +323,18 @@ def main():
         "data": "synthetic (seeded on-device generator; random-init 4-bit g64 weights)",
         "config": {"workload": "qwen2.5-0.5b decode step, linear layers only: 24 x {q 896->896, k 896->128, "
                                "v 896->128, o 896->896, gate 896->4864, up 896->4864, down 4864->896} + "
-                               "lm_head 896->151936; M=1, 4-bit, group 64, bf16 x/scales/biases/y",
-                   "launches_per_step": len(shapes), "bytes_per_step": step_bytes,
+                               "lm_head 896->151936; M=1, 4-bit, group 64, bf16 x/scales/biases/y; "
+                               "q/k/v and gate/up as one grouped call each",
+                   "launches_per_step": 97, "bytes_per_step": step_bytes,
                    "weight_replicas": args.replicas, "hip_graph": True},
         "roofline": {"kernel": "lm_head 896->151936 M=1 (qmvx_kernel<4, 0, 1, 6>: 4-bit, bf16 scales, 1 row of x, group 64)", "bound": "hbm",
                      "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "avg_launch_us": round(lm_avg * 1e6, 3), "bytes_per_launch": lm_bytes},
     }
-    print(f"# step {ms_per_step * 1e3:.1f} us, {gbs:.1f} GB/s; lm_head {lm_avg * 1e6:.2f} us {lm_gbs:.1f} GB/s",
+    out["step_one_launch_per_projection"] = single
+    print(f"# step {ms_per_step * 1e3:.1f} us, {gbs:.1f} GB/s (one launch per projection: "
+          f"{single['us_per_step']:.1f} us); lm_head {lm_avg * 1e6:.2f} us {lm_gbs:.1f} GB/s",
           file=sys.stderr, flush=True)
     del graphs, replicas
     torch.cuda.empty_cache()

@@ -74,6 +74,34 @@ int miqmm_quantized_matmul(void* y, const void* x, const uint32_t* w, const void
                            void* stream);
 
 /*
+ * One projection of a grouped call: y = quantized_matmul(x, w, scales, biases)
+ * (+ bias when non-null), N output rows.
+ */
+typedef struct miqmm_problem {
+    void* y;
+    const void* x;
+    const uint32_t* w;
+    const void* scales;
+    const void* biases;
+    const void* bias;
+    int64_t N;
+} miqmm_problem;
+
+/*
+ * Several independent projections that share M, K, group_size, bits and
+ * dtypes, as one v_dot2 GEMV launch per four problems when M <= 2 and every
+ * N < 65536 (decode projections), else one call per problem on its own route.  This has no single counterpart
+ * in the reference: it replaces the reference's separate quantized projections
+ * that read the same activation -- q/k/v (src/engine/mlx_lm/models/llama.rs:
+ * 195-197) and gate/up (:293-294) -- whose decode-step launches are otherwise
+ * latency-bound.  Each problem's result equals miqmm_quantized_matmul (or
+ * miqmm_quantized_linear when bias is set) on it alone.
+ */
+int miqmm_quantized_matmul_grouped(const miqmm_problem* problems, int count, int64_t M, int64_t K,
+                                   int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
+                                   void* stream);
+
+/*
  * As miqmm_quantized_matmul, with the route forced (MIQMM_ROUTE_QMV and
  * MIQMM_ROUTE_QMV_DOT accept any M, one pass over W per 16 rows of x;
  * MIQMM_ROUTE_QMM any M >= 1).

@@ -74,9 +74,12 @@ int auto_route(int64_t M, int64_t N, int64_t K, int group_size) {
     return M <= 16 ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
 }
 
-int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
-               const void* bias, int64_t M, int64_t N, int64_t K, int transpose, int group_size,
-               int bits, int x_dtype, int sb_dtype, int y_dtype, int route, void* stream) {
+// argument checks shared by the single and grouped entry points; MIQMM_OK
+// with *noop set when M == 0
+int check_args(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases, int64_t M,
+               int64_t N, int64_t K, int transpose, int group_size, int bits, int x_dtype, int sb_dtype,
+               int y_dtype, int route, bool* noop) {
+    *noop = false;
     if (!transpose)
         return fail(MIQMM_ENOTSUP, "transpose=false is not provided (every live call site uses transpose=true)");
     int st = check_quant(N, K, group_size, bits, sb_dtype);
@@ -90,12 +93,25 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
         return fail(MIQMM_EINVAL, "route %d invalid", route);
     if (route == MIQMM_ROUTE_QMVX && !miqmm::qmvx_supported(M < 4 ? M : 4, K, group_size))
         return fail(MIQMM_ENOTSUP, "route qmvx needs K/group_size even and min(M,4)*K <= 32768");
-    if (M == 0) return ok();
+    if (M == 0) {
+        *noop = true;
+        return ok();
+    }
     if (!y || !x || !w || !scales || !biases) return fail(MIQMM_EINVAL, "null pointer argument");
     if (!aligned16(x) || !aligned16(w))
         return fail(MIQMM_EINVAL, "x and w must be 16-byte aligned");
     if (M * K >= ((int64_t)1 << 40) || M * N >= ((int64_t)1 << 40))
         return fail(MIQMM_EINVAL, "M*K or M*N too large");
+    return ok();
+}
+
+int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+               const void* bias, int64_t M, int64_t N, int64_t K, int transpose, int group_size,
+               int bits, int x_dtype, int sb_dtype, int y_dtype, int route, void* stream) {
+    bool noop;
+    int st = check_args(y, x, w, scales, biases, M, N, K, transpose, group_size, bits, x_dtype, sb_dtype, y_dtype,
+                        route, &noop);
+    if (st != MIQMM_OK || noop) return st;
 
     miqmm::QmmArgs a{y, x, w, scales, biases, bias, M, N, K, group_size, bits, x_dtype, sb_dtype, y_dtype,
                      reinterpret_cast<hipStream_t>(stream)};
@@ -146,6 +162,46 @@ int miqmm_quantized_linear(void* y, const void* x, const uint32_t* w, const void
                            void* stream) {
     return qmm_common(y, x, w, scales, biases, bias, M, N, K, 1, group_size, bits, x_dtype, sb_dtype,
                       y_dtype, MIQMM_ROUTE_AUTO, stream);
+}
+
+int miqmm_quantized_matmul_grouped(const miqmm_problem* problems, int count, int64_t M, int64_t K,
+                                   int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
+                                   void* stream) {
+    if (count < 0 || (count > 0 && !problems)) return fail(MIQMM_EINVAL, "problems must hold count >= 0 entries");
+    // decode-sized projections (M <= 2, none of them a wide head) run as one
+    // grouped v_dot2 GEMV launch per four: at these sizes the launches are
+    // latency-bound, so fewer of them beat a faster per-shape route
+    bool grouped = M >= 1 && M <= 2;
+    for (int i = 0; i < count; ++i) {
+        const miqmm_problem& p = problems[i];
+        bool noop;
+        const int st = check_args(p.y, p.x, p.w, p.scales, p.biases, M, p.N, K, 1, group_size, bits, x_dtype,
+                                  sb_dtype, y_dtype, MIQMM_ROUTE_AUTO, &noop);
+        if (st != MIQMM_OK) return st;
+        if (p.N >= 65536) grouped = false;
+    }
+    if (M == 0 || count == 0) return ok();
+    if (!grouped) {  // one call per problem on its own route
+        for (int i = 0; i < count; ++i) {
+            const miqmm_problem& p = problems[i];
+            const int st = qmm_common(p.y, p.x, p.w, p.scales, p.biases, p.bias, M, p.N, K, 1, group_size, bits,
+                                      x_dtype, sb_dtype, y_dtype, MIQMM_ROUTE_AUTO, stream);
+            if (st != MIQMM_OK) return st;
+        }
+        return ok();
+    }
+    for (int i0 = 0; i0 < count; i0 += miqmm::kMaxGroup) {
+        miqmm::QmmArgs a[miqmm::kMaxGroup];
+        const int n = count - i0 < miqmm::kMaxGroup ? count - i0 : miqmm::kMaxGroup;
+        for (int i = 0; i < n; ++i) {
+            const miqmm_problem& p = problems[i0 + i];
+            a[i] = miqmm::QmmArgs{p.y, p.x, p.w, p.scales, p.biases, p.bias, M, p.N, K, group_size, bits,
+                                  x_dtype, sb_dtype, y_dtype, reinterpret_cast<hipStream_t>(stream)};
+        }
+        const int st = check_launch(miqmm::launch_qmv_grouped(a, n), "grouped qmv_dot launch");
+        if (st != MIQMM_OK) return st;
+    }
+    return ok();
 }
 
 int miqmm_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,

@@ -19,8 +19,29 @@ struct QmmArgs {
     hipStream_t stream;
 };
 
+// Up to kMaxGroup independent GEMV problems sharing M, K, group size, bits and
+// dtypes, run as one grid (kernel argument, passed by value): problem p owns
+// the row tiles [tile0[p], tile0[p+1]).
+constexpr int kMaxGroup = 4;
+struct GemvProblem {  // one problem's fields together: a single-problem kernel reads one contiguous run
+    const void* x;
+    const uint32_t* w;
+    const void* s;
+    const void* b;
+    void* y;
+    const void* bias;
+    int n;
+    int tile0;  // first row tile of this problem in the grid
+};
+struct GemvProblems {
+    GemvProblem p[kMaxGroup];
+    int tiles;  // row tiles of all problems
+    int count;
+};
+
 // route launchers; return hipSuccess or the launch error
 hipError_t launch_qmv(const QmmArgs& a);       // VALU dot2 GEMV
+hipError_t launch_qmv_grouped(const QmmArgs* a, int count);  // same, count <= kMaxGroup problems
 hipError_t launch_qmv_mfma(const QmmArgs& a);  // group-diagonal MFMA GEMV
 hipError_t launch_qmm(const QmmArgs& a);
 hipError_t launch_qmvx(const QmmArgs& a);      // MFMA GEMV, M <= 4, x in LDS

@@ -46,13 +46,16 @@ struct Stage {
     uint32_t xoff;  // byte offset of this chunk in row 0 of x, or kOOB past the row end
 };
 
-template <int BITS, int SBT, int MT, int L, int R>
-__global__ __launch_bounds__(256) void qmv_kernel(const uint16_t* __restrict__ x,
-                                                  const uint32_t* __restrict__ w,
-                                                  const uint16_t* __restrict__ sc,
-                                                  const uint16_t* __restrict__ bi,
-                                                  void* __restrict__ y, const void* __restrict__ bias,
-                                                  int M, int N, int K, int gs_shift, int y_dtype) {
+// problem p of the kernel-argument table, p wave-uniform: a select chain
+// rather than an index, which would copy the table to scratch
+__device__ __forceinline__ const GemvProblem& pick4(const GemvProblems& P, int p) {
+    return p == 0 ? P.p[0] : p == 1 ? P.p[1] : p == 2 ? P.p[2] : P.p[3];
+}
+
+// GRP: P holds several problems (P.count of them); otherwise exactly one, and
+// every lookup below folds to problem 0 at compile time
+template <int BITS, int SBT, int MT, int L, int R, bool GRP>
+__global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, int K, int gs_shift, int y_dtype) {
     constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk: 32 or 16
     constexpr int CPC = 1 << CPC_SHIFT;
     constexpr int NP = CPC / 2;
@@ -68,18 +71,27 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint16_t* __restrict__ x
     const int nwaves = gridDim.x * 4;
     const int C = K >> CPC_SHIFT;
     const int J = (C + L - 1) / L;  // chunk iterations per row
-    const int tiles = (N + TILE - 1) / TILE;
+    const int tiles = P.tiles;
+    // problem owning a tile (tiles of problem p: [tile0[p], tile0[p+1]))
+    auto prob_of = [&](int tile) {
+        int p = 0;
+        if constexpr (GRP) {
+#pragma unroll
+            for (int i = 1; i < kMaxGroup; ++i) p += (i < P.count && tile >= P.p[i].tile0) ? 1 : 0;
+            p = __builtin_amdgcn_readfirstlane(p);
+        }
+        return p;
+    };
     const int my_tiles = gwave < tiles ? (tiles - 1 - gwave) / nwaves + 1 : 0;
     const int iters = my_tiles * J;
     if (iters == 0) return;  // wave-uniform
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
     const uint32_t xrow_bytes = (uint32_t)K * 2;
-    const auto xr = make_rsrc(x, (uint32_t)M * xrow_bytes);
     const uint32_t kMask = vgpr_const(0x000F000Fu), kMagic = kMagic128x2;
 
     // x of one chunk position for every row of x (zero past the row end or m >= M)
-    auto load_x = [&](uint32_t xoff, uint32_t (*xw)[NP]) {
+    auto load_x = [&](__amdgpu_buffer_rsrc_t xr, uint32_t xoff, uint32_t (*xw)[NP]) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const uint32_t off = m < M ? xoff + (uint32_t)m * xrow_bytes : kOOB;
@@ -119,12 +131,15 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint16_t* __restrict__ x
             j_i = 0;
             tile_i += nwaves;
         }
-        const int rows_left = N - tile * TILE;
+        const int p = prob_of(tile);
+        const GemvProblem& pp = pick4(P, p);
+        const int lt = tile - pp.tile0;  // tile within its problem
+        const int rows_left = pp.n - lt * TILE;
         const uint32_t valid_rows = (uint32_t)(rows_left < TILE ? rows_left : TILE);
         // resources rebased on the tile: 32-bit offsets, and rows past N read as zero
-        const auto wr = make_rsrc((const char*)w + (size_t)tile * TILE * row_bytes, valid_rows * row_bytes);
-        const auto sr = make_rsrc(sc + (size_t)tile * TILE * G, valid_rows * G * 2);
-        const auto br = make_rsrc(bi + (size_t)tile * TILE * G, valid_rows * G * 2);
+        const auto wr = make_rsrc((const char*)pp.w + (size_t)lt * TILE * row_bytes, valid_rows * row_bytes);
+        const auto sr = make_rsrc((const uint16_t*)pp.s + (size_t)lt * TILE * G, valid_rows * G * 2);
+        const auto br = make_rsrc((const uint16_t*)pp.b + (size_t)lt * TILE * G, valid_rows * G * 2);
         const bool cv = c < C;
         const uint32_t g = (uint32_t)((c << CPC_SHIFT) >> gs_shift);
 #pragma unroll
@@ -135,7 +150,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint16_t* __restrict__ x
             st.b[r] = bload2(br, (row * G + g) * 2);
         }
         st.xoff = cv ? (uint32_t)c * CPC * 2 : kOOB;
-        if constexpr (XPF) load_x(st.xoff, st.xw);
+        if constexpr (XPF) load_x(make_rsrc(pp.x, (uint32_t)M * xrow_bytes), st.xoff, st.xw);
     };
 
     float acc[R][MT];
@@ -151,7 +166,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint16_t* __restrict__ x
             prep_x(st.xw, X, xs);
         } else {
             uint32_t xw[MT][NP];
-            load_x(st.xoff, xw);
+            const int pc = prob_of(tile_c);
+            load_x(make_rsrc(pick4(P, pc).x, (uint32_t)M * xrow_bytes), st.xoff, xw);
             prep_x(xw, X, xs);
         }
 #pragma unroll
@@ -175,7 +191,11 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint16_t* __restrict__ x
             }
         }
         if (++j_c == J) {  // tile complete: reduce over the sub-group and store
-            const int row0 = tile_c * TILE + sg * R;
+            const GemvProblem& pc = pick4(P, prob_of(tile_c));
+            const int N = pc.n;
+            void* const y = pc.y;
+            const void* const bias = pc.bias;
+            const int row0 = (tile_c - pc.tile0) * TILE + sg * R;
             j_c = 0;
             tile_c += nwaves;
 #pragma unroll
@@ -205,17 +225,33 @@ __global__ __launch_bounds__(256) void qmv_kernel(const uint16_t* __restrict__ x
     }
 }
 
+// a[0..count) share M, K, group size, bits and dtypes; one grid covers all
+// (grouped grids are built for one or two rows of x only)
 template <int BITS, int SBT, int MT, int L, int R>
-hipError_t launch_t(const QmmArgs& a) {
+hipError_t launch_t(const QmmArgs* a, int count) {
+    if (count > 1 && MT > 2) return hipErrorInvalidValue;
     constexpr int TILE = (64 / L) * R;
-    const int64_t tiles = (a.N + TILE - 1) / TILE;
+    GemvProblems P{};
+    P.count = count;
+    int64_t tiles = 0;
+    for (int i = 0; i < kMaxGroup; ++i) {
+        const QmmArgs& q = a[i < count ? i : count - 1];  // unused slots repeat the last problem
+        P.p[i] = GemvProblem{q.x, q.w, q.scales, q.biases, q.y, q.bias, (int)q.N, (int)tiles};
+        if (i < count) tiles += (q.N + TILE - 1) / TILE;
+    }
+    P.tiles = (int)tiles;
     const int64_t want = (tiles + 3) / 4;
     const int blocks = (int)(want < kNumCUs * kMaxBlocksPerCU ? want : kNumCUs * kMaxBlocksPerCU);
-    const int gs_shift = __builtin_ctz((unsigned)a.group_size);
-    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R>), dim3(blocks), dim3(256), 0, a.stream,
-                       (const uint16_t*)a.x, a.w, (const uint16_t*)a.scales,
-                       (const uint16_t*)a.biases, a.y, a.bias, (int)a.M, (int)a.N, (int)a.K,
-                       gs_shift, a.y_dtype);
+    const int gs_shift = __builtin_ctz((unsigned)a[0].group_size);
+    if constexpr (MT <= 2) {
+        if (count > 1) {
+            hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, true>), dim3(blocks), dim3(256), 0, a[0].stream, P,
+                               (int)a[0].M, (int)a[0].K, gs_shift, a[0].y_dtype);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, false>), dim3(blocks), dim3(256), 0, a[0].stream, P,
+                       (int)a[0].M, (int)a[0].K, gs_shift, a[0].y_dtype);
     return hipGetLastError();
 }
 
@@ -242,22 +278,22 @@ int pick_l(int64_t K, int bits) {
 int pick_r(int64_t M) { return M <= 2 ? 4 : M <= 4 ? 2 : 1; }
 
 template <int BITS, int SBT, int MT, int R>
-hipError_t launch_l(const QmmArgs& a) {
-    switch (pick_l(a.K, a.bits)) {
-        case 16: return launch_t<BITS, SBT, MT, 16, R>(a);
-        case 32: return launch_t<BITS, SBT, MT, 32, R>(a);
-        default: return launch_t<BITS, SBT, MT, 64, R>(a);
+hipError_t launch_l(const QmmArgs* a, int count) {
+    switch (pick_l(a[0].K, a[0].bits)) {
+        case 16: return launch_t<BITS, SBT, MT, 16, R>(a, count);
+        case 32: return launch_t<BITS, SBT, MT, 32, R>(a, count);
+        default: return launch_t<BITS, SBT, MT, 64, R>(a, count);
     }
 }
 
 template <int BITS, int SBT>
-hipError_t launch_mt(const QmmArgs& a) {
-    switch (pick_mt(a.M)) {
-        case 1: return launch_l<BITS, SBT, 1, 4>(a);
-        case 2: return launch_l<BITS, SBT, 2, 4>(a);
-        case 4: return launch_l<BITS, SBT, 4, 2>(a);
-        case 8: return launch_l<BITS, SBT, 8, 1>(a);
-        default: return launch_l<BITS, SBT, 16, 1>(a);
+hipError_t launch_mt(const QmmArgs* a, int count) {
+    switch (pick_mt(a[0].M)) {
+        case 1: return launch_l<BITS, SBT, 1, 4>(a, count);
+        case 2: return launch_l<BITS, SBT, 2, 4>(a, count);
+        case 4: return launch_l<BITS, SBT, 4, 2>(a, count);
+        case 8: return launch_l<BITS, SBT, 8, 1>(a, count);
+        default: return launch_l<BITS, SBT, 16, 1>(a, count);
     }
 }
 
@@ -269,10 +305,13 @@ void qmv_config(const QmmArgs& a, int* rows_per_subgroup, int* m_tile, int* lane
     if (lanes_per_row) *lanes_per_row = pick_l(a.K, a.bits);
 }
 
-hipError_t launch_qmv(const QmmArgs& a) {
-    if (a.bits == 4)
-        return a.sb_dtype == DT_F16 ? launch_mt<4, DT_F16>(a) : launch_mt<4, DT_BF16>(a);
-    return a.sb_dtype == DT_F16 ? launch_mt<8, DT_F16>(a) : launch_mt<8, DT_BF16>(a);
+hipError_t launch_qmv_grouped(const QmmArgs* a, int count) {
+    if (count < 1 || count > kMaxGroup) return hipErrorInvalidValue;
+    if (a[0].bits == 4)
+        return a[0].sb_dtype == DT_F16 ? launch_mt<4, DT_F16>(a, count) : launch_mt<4, DT_BF16>(a, count);
+    return a[0].sb_dtype == DT_F16 ? launch_mt<8, DT_F16>(a, count) : launch_mt<8, DT_BF16>(a, count);
 }
+
+hipError_t launch_qmv(const QmmArgs& a) { return launch_qmv_grouped(&a, 1); }
 
 }  // namespace miqmm

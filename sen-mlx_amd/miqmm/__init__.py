@@ -28,7 +28,8 @@ import torch
 
 __all__ = [
     "MiqmmError", "quantized_matmul", "quantized_linear", "QuantizedLinear", "dequantize",
-    "unpack", "synth_problem", "query_route", "result_type", "lib", "LIB_PATH",
+    "unpack", "synth_problem", "query_route", "result_type", "lib", "LIB_PATH", "quantized_matmul_grouped",
+    "Problem",
     "OK", "EINVAL", "ENOTSUP", "EHIP", "ROUTE_AUTO", "ROUTE_QMV", "ROUTE_QMM", "ROUTE_QMV_DOT", "ROUTE_QMVX",
 ]
 
@@ -52,6 +53,13 @@ class MiqmmError(RuntimeError):
 _lib = None
 
 
+class Problem(ctypes.Structure):
+    """miqmm_problem: one projection of a grouped call"""
+    _fields_ = [("y", ctypes.c_void_p), ("x", ctypes.c_void_p), ("w", ctypes.c_void_p),
+                ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+                ("N", ctypes.c_int64)]
+
+
 def lib() -> ctypes.CDLL:
     """the loaded libmiqmm.so (raises if it has not been built)"""
     global _lib
@@ -68,8 +76,10 @@ def lib() -> ctypes.CDLL:
     L.miqmm_unpack.argtypes = [P, P, I64, I64, I, P]
     L.miqmm_query_route.argtypes = [I64, I64, I64, I, I, ctypes.POINTER(I), ctypes.POINTER(I)]
     L.miqmm_synth_problem.argtypes = [P, P, P, P, I64, I64, I64, I, I, I, I, U64, U64, P]
+    L.miqmm_quantized_matmul_grouped.argtypes = [ctypes.POINTER(Problem), I, I64, I64, I, I, I, I, I, P]
     for name in ("miqmm_quantized_matmul", "miqmm_quantized_matmul_ex", "miqmm_quantized_linear",
-                 "miqmm_dequantize", "miqmm_unpack", "miqmm_query_route", "miqmm_synth_problem"):
+                 "miqmm_dequantize", "miqmm_unpack", "miqmm_query_route", "miqmm_synth_problem",
+                 "miqmm_quantized_matmul_grouped"):
         getattr(L, name).restype = I
     L.miqmm_last_error.argtypes, L.miqmm_last_error.restype = [], ctypes.c_char_p
     L.miqmm_version.argtypes, L.miqmm_version.restype = [], ctypes.c_char_p
@@ -156,6 +166,52 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
                                            K, int(bool(transpose)), group_size, bits, _dt(xc), _dt(scales),
                                            _dt(out), route, _stream(stream)))
     return out
+
+
+def quantized_matmul_grouped(xs, ws, scales, biases, group_size: int = 64, bits: int = 4, *,
+                             outs=None, bias=None, stream=None):
+    """[quantized_matmul(xs[i], ws[i], scales[i], biases[i]) (+ bias[i])] as one
+    launch per four projections where the route allows (decode, M <= 2).  The
+    projections share M, K, group size, bits and dtypes -- the reference's
+    q/k/v (src/engine/mlx_lm/models/llama.rs:195-197) and gate/up (:293-294)."""
+    n = len(ws)
+    if not (len(xs) == len(scales) == len(biases) == n):
+        raise MiqmmError(EINVAL, "xs, ws, scales and biases must have the same length")
+    if n == 0:
+        return []
+    bias = list(bias) if bias is not None else [None] * n
+    outs = list(outs) if outs is not None else [None] * n
+    probs = (Problem * n)()
+    keep = []
+    M = K = None
+    for i in range(n):
+        N, Ki = _check_weights(ws[i], scales[i], biases[i], group_size, bits)
+        x = xs[i]
+        if x.shape[-1] != Ki:
+            raise MiqmmError(EINVAL, f"x[{i}] inner dim {x.shape[-1]} != K={Ki}")
+        xc = x.contiguous()
+        Mi = xc.numel() // Ki
+        if M is None:
+            M, K = Mi, Ki
+        elif (Mi, Ki) != (M, K) or scales[i].dtype != scales[0].dtype or xs[i].dtype != xs[0].dtype:
+            raise MiqmmError(EINVAL, "grouped projections must share M, K and dtypes")
+        shape = tuple(x.shape[:-1]) + (N,)
+        ydt = result_type(x.dtype, scales[i].dtype)
+        if outs[i] is None:
+            outs[i] = torch.empty(shape, dtype=ydt, device=x.device)
+        elif outs[i].shape != shape or not outs[i].is_contiguous() or outs[i].dtype != ydt:
+            raise MiqmmError(EINVAL, f"outs[{i}] must be contiguous {shape} of {ydt}")
+        b = bias[i]
+        if b is not None:
+            if b.shape != (N,) or b.dtype != ydt:
+                raise MiqmmError(EINVAL, f"bias[{i}] must be [{N}] of dtype {ydt}")
+            b = b.contiguous()
+        keep += [xc, b]
+        probs[i] = Problem(outs[i].data_ptr(), xc.data_ptr(), ws[i].data_ptr(), scales[i].data_ptr(),
+                           biases[i].data_ptr(), None if b is None else b.data_ptr(), N)
+    _check(lib().miqmm_quantized_matmul_grouped(probs, n, M, K, group_size, bits, _dt(xs[0].contiguous()),
+                                                _dt(scales[0]), _dt(outs[0]), _stream(stream)))
+    return outs
 
 
 def quantized_linear(x, w, scales, biases, bias=None, group_size: int = 64, bits: int = 4, **kw):

@@ -85,6 +85,24 @@ def test_other_entry_points_validate(lib):
     assert lib.miqmm_quantized_linear(None, P, P, P, P, None, 1, 8, 128, 64, 4, 0, 0, 0, None) == 1
 
 
+def test_grouped_entry_point_validates(lib):
+    import miqmm
+
+    G = lib.miqmm_quantized_matmul_grouped
+    assert G(None, -1, 1, 128, 64, 4, 0, 0, 0, None) == miqmm.EINVAL
+    assert G(None, 2, 1, 128, 64, 4, 0, 0, 0, None) == miqmm.EINVAL  # no table for two problems
+    assert G(None, 0, 1, 128, 64, 4, 0, 0, 0, None) == miqmm.OK      # nothing to do
+    probs = (miqmm.Problem * 2)()
+    probs[0] = miqmm.Problem(16, 16, 16, 16, 16, None, 8)
+    probs[1] = miqmm.Problem(16, 16, 16, 16, 16, None, 8)
+    assert G(probs, 2, 1, 96, 64, 4, 0, 0, 0, None) == miqmm.EINVAL  # K % group_size != 0
+    assert G(probs, 2, 1, 128, 64, 3, 0, 0, 0, None) == miqmm.ENOTSUP
+    probs[1] = miqmm.Problem(None, 16, 16, 16, 16, None, 8)
+    assert G(probs, 2, 1, 128, 64, 4, 0, 0, 0, None) == miqmm.EINVAL  # null y in the second problem
+    assert b"null" in lib.miqmm_last_error()
+    assert G(probs, 2, 0, 128, 64, 4, 0, 0, 0, None) == miqmm.OK      # M == 0 is a no-op
+
+
 def test_query_route(lib):
     import miqmm
 
