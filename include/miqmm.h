@@ -124,6 +124,28 @@ int miqmm_quantized_linear(void* y, const void* x, const uint32_t* w, const void
                            void* stream);
 
 /*
+ * Expert-gathered quantized matmul:
+ *   y[b, j] = x[b or (b, j)] @ dequant(w[rhs_indices[b, j]]).T
+ * for b < batch, j < top_k, each product an M x N matrix (b-major, then j).
+ * w: the stacked experts, [experts, N, K*bits/32] uint32; scales / biases
+ * [experts, N, K/group_size].  rhs_indices: [batch, top_k] int32 on the
+ * device.  x_per_index = 0: x holds batch matrices [M, K], each shared by
+ * its top_k selections (the SwitchGLU gate / up projections,
+ * x [..., 1, 1, K]); 1: x holds batch*top_k matrices, one per selection
+ * (the down projection, h [..., top_k, 1, K]).  An index outside
+ * [0, experts) yields zero rows instead of an out-of-bounds read.
+ * sorted_indices is accepted as a hint and changes nothing.
+ * Replaces mlx_sys::mlx_gather_qmm as wrapped by
+ * src/engine/mlx_lm/utils/moe.rs:33-77 (lhs_indices absent, transpose=true),
+ * called from src/engine/mlx_lm/models/deepseek_v2.rs:430-442 and
+ * src/engine/mlx_lm/models/gemma4.rs:770-782.
+ */
+int miqmm_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                     const int32_t* rhs_indices, int64_t batch, int64_t top_k, int x_per_index, int64_t M,
+                     int64_t N, int64_t K, int64_t experts, int transpose, int group_size, int bits, int x_dtype,
+                     int sb_dtype, int y_dtype, int sorted_indices, void* stream);
+
+/*
  * out[n, k] = scales[n,k/g] * q[n,k] + biases[n,k/g] (fp32 fma, stored as
  * out_dtype).  Replaces mlx_rs::ops::dequantize as used beside the
  * reference's quantized-matmul test (src/engine/mlx_lm/utils/moe.rs:118-126).

@@ -11,6 +11,8 @@ Reference citations (SenClaw/sen-mlx tree):
     (bits=1), generalised to bits 4 and 8.
   - shapes w [N, K*bits/32], scales/biases [N, K/g]: src/engine/mlx_lm/utils/moe.rs:20-31.
   - dequant fma(scale, q, bias) in fp32: src/engine/mlx_lm/models/bonsai_q1.rs:172.
+  - gather_qmm (stacked experts [E, N, ...] selected per batch entry):
+    src/engine/mlx_lm/utils/moe.rs:20-31, test at moe.rs:84-146.
 
 The generator is the same splitmix64 counter hash + Irwin-Hall(4) normal as the
 C oracle; every float step is a single IEEE fp32 operation, so numpy, C and HIP
@@ -157,6 +159,28 @@ def dequantize(w, s, b, K, group_size, bits, sb_dtype=BF16, exact=False) -> np.n
 def qmm_f64(x, w, s, b, K, group_size, bits, x_dtype=BF16, sb_dtype=BF16) -> np.ndarray:
     wd = dequantize(w, s, b, K, group_size, bits, sb_dtype, exact=True)
     return half_to_f32(x, x_dtype).astype(np.float64) @ wd.T
+
+
+def gather_qmm_f64(x, w, s, b, idx, K, group_size, bits, x_dtype=BF16, sb_dtype=BF16) -> np.ndarray:
+    """out[i] = x[i] @ dequant(w[idx[i]]).T over the broadcast batch i (float64).
+
+    Restates the gather_qmm wrapper's contract (src/engine/mlx_lm/utils/moe.rs:20-31,
+    lhs_indices absent, transpose=true): w [E, N, K*bits/32], s/b [E, N, K/g],
+    x [..., M, K] whose batch dims broadcast against idx [...]; the result is
+    [*broadcast, M, N].  An index outside [0, E) gives zero rows (MLX leaves it
+    undefined; the library defines it this way)."""
+    x = np.asarray(x)
+    idx = np.asarray(idx)
+    E, N = w.shape[0], w.shape[1]
+    M = x.shape[-2]
+    bshape = np.broadcast_shapes(x.shape[:-2], idx.shape)
+    xb = np.broadcast_to(x, bshape + (M, K)).reshape(-1, M, K)
+    ib = np.broadcast_to(idx, bshape).reshape(-1)
+    out = np.zeros((ib.size, M, N), np.float64)
+    for i, e in enumerate(ib.tolist()):
+        if 0 <= e < E:
+            out[i] = qmm_f64(xb[i], w[e], s[e], b[e], K, group_size, bits, x_dtype, sb_dtype)
+    return out.reshape(bshape + (M, N))
 
 
 # ---------------------------------------------------------------- tolerance

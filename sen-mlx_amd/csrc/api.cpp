@@ -204,6 +204,39 @@ int miqmm_quantized_matmul_grouped(const miqmm_problem* problems, int count, int
     return ok();
 }
 
+int miqmm_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                     const int32_t* rhs_indices, int64_t batch, int64_t top_k, int x_per_index, int64_t M,
+                     int64_t N, int64_t K, int64_t experts, int transpose, int group_size, int bits, int x_dtype,
+                     int sb_dtype, int y_dtype, int sorted_indices, void* stream) {
+    (void)sorted_indices;  // a scheduling hint only: every order gives the same result here
+    if (batch < 0 || top_k < 0 || batch >= kMaxDim || top_k >= kMaxDim)
+        return fail(MIQMM_EINVAL, "batch and top_k must be in [0, 2^31), got %lld and %lld", (long long)batch,
+                    (long long)top_k);
+    if (experts <= 0 || experts >= kMaxDim)
+        return fail(MIQMM_EINVAL, "experts must be in [1, 2^31), got %lld", (long long)experts);
+    if (x_per_index != 0 && x_per_index != 1) return fail(MIQMM_EINVAL, "x_per_index must be 0 or 1");
+    const int64_t problems = batch * top_k;
+    bool noop;  // no selections or no rows: nothing to read, pointers may be null
+    int st = check_args(y, x, w, scales, biases, problems == 0 ? 0 : M, N, K, transpose, group_size, bits, x_dtype,
+                        sb_dtype, y_dtype, MIQMM_ROUTE_AUTO, &noop);
+    if (st != MIQMM_OK || noop) return st;
+    if (!rhs_indices) return fail(MIQMM_EINVAL, "null pointer argument");
+    if (problems * M * (K > N ? K : N) >= ((int64_t)1 << 40)) return fail(MIQMM_EINVAL, "batch*top_k*M*K too large");
+    // the GEMV handles 16 rows of x per pass over a weight tile; more rows
+    // (rare in decode) take several passes, one per 16-row slice of every matrix
+    const int ysz = y_dtype == MIQMM_DT_F32 ? 4 : 2;
+    for (int64_t m0 = 0; m0 < M; m0 += 16) {
+        miqmm::QmmArgs a{static_cast<char*>(y) + m0 * N * ysz, static_cast<const uint16_t*>(x) + m0 * K, w, scales,
+                         biases, nullptr, M - m0 < 16 ? M - m0 : 16, N, K, group_size, bits, x_dtype, sb_dtype,
+                         y_dtype, reinterpret_cast<hipStream_t>(stream)};
+        st = check_launch(
+            miqmm::launch_qmv_gather(a, rhs_indices, batch, (int)top_k, x_per_index, experts, M * K, M * N),
+            "gather qmv launch");
+        if (st != MIQMM_OK) return st;
+    }
+    return ok();
+}
+
 int miqmm_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
                      int64_t N, int64_t K, int group_size, int bits, int sb_dtype, int out_dtype,
                      void* stream) {

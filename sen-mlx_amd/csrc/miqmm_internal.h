@@ -37,11 +37,22 @@ struct GemvProblems {
     GemvProblem p[kMaxGroup];
     int tiles;  // row tiles of all problems
     int count;
+    // gather mode (MoE experts): problem b = (token b / top_k, slot b % top_k)
+    // multiplies its x by expert idx[b] of the stacked weights in p[0]
+    const int32_t* idx;
+    int top_k, x_per_expert, experts, tiles_per_problem;
+    int64_t x_stride, y_stride;  // elements between consecutive x / y matrices
 };
 
 // route launchers; return hipSuccess or the launch error
 hipError_t launch_qmv(const QmmArgs& a);       // VALU dot2 GEMV
 hipError_t launch_qmv_grouped(const QmmArgs* a, int count);  // same, count <= kMaxGroup problems
+// expert-gathered GEMVs: a describes one expert (w/scales/biases = expert 0 of
+// the stack), x holds T*(x_per_expert ? top_k : 1) matrices, y holds T*top_k
+// matrices of N columns, x_stride / y_stride elements apart; a.M <= 16 rows of
+// each are computed; idx is [T, top_k] on the device
+hipError_t launch_qmv_gather(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_expert,
+                             int64_t experts, int64_t x_stride, int64_t y_stride);
 hipError_t launch_qmv_mfma(const QmmArgs& a);  // group-diagonal MFMA GEMV
 hipError_t launch_qmm(const QmmArgs& a);
 hipError_t launch_qmvx(const QmmArgs& a);      // MFMA GEMV, M <= 4, x in LDS

@@ -52,9 +52,20 @@ __device__ __forceinline__ const GemvProblem& pick4(const GemvProblems& P, int p
     return p == 0 ? P.p[0] : p == 1 ? P.p[1] : p == 2 ? P.p[2] : P.p[3];
 }
 
-// GRP: P holds several problems (P.count of them); otherwise exactly one, and
-// every lookup below folds to problem 0 at compile time
-template <int BITS, int SBT, int MT, int L, int R, bool GRP>
+// where one row tile of the grid reads and writes
+struct TileRef {
+    const void* x;
+    const char* w;       // first code byte of the tile's first row
+    const uint16_t* s;   // scales / biases of the tile's first row
+    const uint16_t* b;
+    char* y;             // the problem's output matrix
+    const void* bias;
+    int N, row0, rows;   // problem rows, first row of the tile, rows present (0: read nothing)
+};
+
+// MODE 0: P holds one problem (every lookup folds to problem 0 at compile
+// time); 1: P.count problems, grouped; 2: expert gather
+template <int BITS, int SBT, int MT, int L, int R, int MODE>
 __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, int K, int gs_shift, int y_dtype) {
     constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk: 32 or 16
     constexpr int CPC = 1 << CPC_SHIFT;
@@ -75,7 +86,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     // problem owning a tile (tiles of problem p: [tile0[p], tile0[p+1]))
     auto prob_of = [&](int tile) {
         int p = 0;
-        if constexpr (GRP) {
+        if constexpr (MODE == 1) {
 #pragma unroll
             for (int i = 1; i < kMaxGroup; ++i) p += (i < P.count && tile >= P.p[i].tile0) ? 1 : 0;
             p = __builtin_amdgcn_readfirstlane(p);
@@ -87,6 +98,41 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     if (iters == 0) return;  // wave-uniform
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
+    const int ysz = y_dtype == DT_F32 ? 4 : 2;
+    auto locate = [&](int tile) {
+        TileRef t;
+        if constexpr (MODE == 2) {
+            const GemvProblem& q = P.p[0];
+            const int b = __builtin_amdgcn_readfirstlane(tile / P.tiles_per_problem);
+            const int lt = tile - b * P.tiles_per_problem;
+            // a scalar load: waiting for it leaves the vector loads in flight
+            const int e = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int32_t*)P.idx)[b]);
+            const bool ok = e >= 0 && e < P.experts;  // an index out of range gives zero rows
+            const int eb = ok ? e : 0;
+            const int xm = P.x_per_expert ? b : b / P.top_k;  // x matrix of this problem
+            t.x = (const uint16_t*)q.x + xm * P.x_stride;
+            t.row0 = lt * TILE;
+            t.w = (const char*)q.w + ((size_t)eb * q.n + t.row0) * row_bytes;
+            t.s = (const uint16_t*)q.s + ((size_t)eb * q.n + t.row0) * G;
+            t.b = (const uint16_t*)q.b + ((size_t)eb * q.n + t.row0) * G;
+            t.y = (char*)q.y + b * P.y_stride * ysz;
+            t.bias = nullptr;
+            t.N = q.n;
+            t.rows = ok ? min(q.n - t.row0, TILE) : 0;
+        } else {
+            const GemvProblem& q = pick4(P, prob_of(tile));
+            t.x = q.x;
+            t.row0 = (tile - q.tile0) * TILE;
+            t.w = (const char*)q.w + (size_t)t.row0 * row_bytes;
+            t.s = (const uint16_t*)q.s + (size_t)t.row0 * G;
+            t.b = (const uint16_t*)q.b + (size_t)t.row0 * G;
+            t.y = (char*)q.y;
+            t.bias = q.bias;
+            t.N = q.n;
+            t.rows = min(q.n - t.row0, TILE);
+        }
+        return t;
+    };
     const uint32_t xrow_bytes = (uint32_t)K * 2;
     const uint32_t kMask = vgpr_const(0x000F000Fu), kMagic = kMagic128x2;
 
@@ -131,15 +177,12 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
             j_i = 0;
             tile_i += nwaves;
         }
-        const int p = prob_of(tile);
-        const GemvProblem& pp = pick4(P, p);
-        const int lt = tile - pp.tile0;  // tile within its problem
-        const int rows_left = pp.n - lt * TILE;
-        const uint32_t valid_rows = (uint32_t)(rows_left < TILE ? rows_left : TILE);
+        const TileRef t = locate(tile);
+        const uint32_t valid_rows = (uint32_t)t.rows;
         // resources rebased on the tile: 32-bit offsets, and rows past N read as zero
-        const auto wr = make_rsrc((const char*)pp.w + (size_t)lt * TILE * row_bytes, valid_rows * row_bytes);
-        const auto sr = make_rsrc((const uint16_t*)pp.s + (size_t)lt * TILE * G, valid_rows * G * 2);
-        const auto br = make_rsrc((const uint16_t*)pp.b + (size_t)lt * TILE * G, valid_rows * G * 2);
+        const auto wr = make_rsrc(t.w, valid_rows * row_bytes);
+        const auto sr = make_rsrc(t.s, valid_rows * G * 2);
+        const auto br = make_rsrc(t.b, valid_rows * G * 2);
         const bool cv = c < C;
         const uint32_t g = (uint32_t)((c << CPC_SHIFT) >> gs_shift);
 #pragma unroll
@@ -150,7 +193,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
             st.b[r] = bload2(br, (row * G + g) * 2);
         }
         st.xoff = cv ? (uint32_t)c * CPC * 2 : kOOB;
-        if constexpr (XPF) load_x(make_rsrc(pp.x, (uint32_t)M * xrow_bytes), st.xoff, st.xw);
+        if constexpr (XPF) load_x(make_rsrc(t.x, (uint32_t)M * xrow_bytes), st.xoff, st.xw);
     };
 
     float acc[R][MT];
@@ -166,8 +209,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
             prep_x(st.xw, X, xs);
         } else {
             uint32_t xw[MT][NP];
-            const int pc = prob_of(tile_c);
-            load_x(make_rsrc(pick4(P, pc).x, (uint32_t)M * xrow_bytes), st.xoff, xw);
+            load_x(make_rsrc(locate(tile_c).x, (uint32_t)M * xrow_bytes), st.xoff, xw);
             prep_x(xw, X, xs);
         }
 #pragma unroll
@@ -191,11 +233,11 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
             }
         }
         if (++j_c == J) {  // tile complete: reduce over the sub-group and store
-            const GemvProblem& pc = pick4(P, prob_of(tile_c));
-            const int N = pc.n;
-            void* const y = pc.y;
-            const void* const bias = pc.bias;
-            const int row0 = (tile_c - pc.tile0) * TILE + sg * R;
+            const TileRef tc = locate(tile_c);
+            const int N = tc.N;
+            void* const y = tc.y;
+            const void* const bias = tc.bias;
+            const int row0 = tc.row0 + sg * R;
             j_c = 0;
             tile_c += nwaves;
 #pragma unroll
@@ -245,13 +287,39 @@ hipError_t launch_t(const QmmArgs* a, int count) {
     const int gs_shift = __builtin_ctz((unsigned)a[0].group_size);
     if constexpr (MT <= 2) {
         if (count > 1) {
-            hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, true>), dim3(blocks), dim3(256), 0, a[0].stream, P,
+            hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 1>), dim3(blocks), dim3(256), 0, a[0].stream, P,
                                (int)a[0].M, (int)a[0].K, gs_shift, a[0].y_dtype);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, false>), dim3(blocks), dim3(256), 0, a[0].stream, P,
+    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 0>), dim3(blocks), dim3(256), 0, a[0].stream, P,
                        (int)a[0].M, (int)a[0].K, gs_shift, a[0].y_dtype);
+    return hipGetLastError();
+}
+
+// a: expert 0's problem (N rows each); T * top_k problems, one per (token, slot)
+template <int BITS, int SBT, int MT, int L, int R>
+hipError_t launch_gather_t(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_expert,
+                           int64_t experts, int64_t x_stride, int64_t y_stride) {
+    constexpr int TILE = (64 / L) * R;
+    GemvProblems P{};
+    P.count = 1;
+    P.p[0] = GemvProblem{a.x, a.w, a.scales, a.biases, a.y, nullptr, (int)a.N, 0};
+    P.idx = idx;
+    P.top_k = top_k;
+    P.x_per_expert = x_per_expert;
+    P.experts = (int)experts;
+    P.tiles_per_problem = (int)((a.N + TILE - 1) / TILE);
+    P.x_stride = x_stride;
+    P.y_stride = y_stride;
+    const int64_t tiles = (int64_t)P.tiles_per_problem * T * top_k;
+    if (tiles >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    P.tiles = (int)tiles;
+    const int64_t want = (tiles + 3) / 4;
+    const int blocks = (int)(want < kNumCUs * kMaxBlocksPerCU ? want : kNumCUs * kMaxBlocksPerCU);
+    const int gs_shift = __builtin_ctz((unsigned)a.group_size);
+    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 2>), dim3(blocks), dim3(256), 0, a.stream, P, (int)a.M,
+                       (int)a.K, gs_shift, a.y_dtype);
     return hipGetLastError();
 }
 
@@ -313,5 +381,39 @@ hipError_t launch_qmv_grouped(const QmmArgs* a, int count) {
 }
 
 hipError_t launch_qmv(const QmmArgs& a) { return launch_qmv_grouped(&a, 1); }
+
+namespace {
+template <int BITS, int SBT, int MT, int R>
+hipError_t gather_l(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int xpe, int64_t E, int64_t xs,
+                    int64_t ys) {
+    switch (pick_l(a.K, a.bits)) {
+        case 16: return launch_gather_t<BITS, SBT, MT, 16, R>(a, idx, T, top_k, xpe, E, xs, ys);
+        case 32: return launch_gather_t<BITS, SBT, MT, 32, R>(a, idx, T, top_k, xpe, E, xs, ys);
+        default: return launch_gather_t<BITS, SBT, MT, 64, R>(a, idx, T, top_k, xpe, E, xs, ys);
+    }
+}
+template <int BITS, int SBT>
+hipError_t gather_mt(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int xpe, int64_t E, int64_t xs,
+                     int64_t ys) {
+    switch (pick_mt(a.M)) {
+        case 1: return gather_l<BITS, SBT, 1, 4>(a, idx, T, top_k, xpe, E, xs, ys);
+        case 2: return gather_l<BITS, SBT, 2, 4>(a, idx, T, top_k, xpe, E, xs, ys);
+        case 4: return gather_l<BITS, SBT, 4, 2>(a, idx, T, top_k, xpe, E, xs, ys);
+        case 8: return gather_l<BITS, SBT, 8, 1>(a, idx, T, top_k, xpe, E, xs, ys);
+        default: return gather_l<BITS, SBT, 16, 1>(a, idx, T, top_k, xpe, E, xs, ys);
+    }
+}
+}  // namespace
+
+hipError_t launch_qmv_gather(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_expert,
+                             int64_t experts, int64_t x_stride, int64_t y_stride) {
+    if (a.M < 1 || a.M > 16) return hipErrorInvalidValue;
+    const int64_t xs = x_stride, ys = y_stride;
+    if (a.bits == 4)
+        return a.sb_dtype == DT_F16 ? gather_mt<4, DT_F16>(a, idx, T, top_k, x_per_expert, experts, xs, ys)
+                                    : gather_mt<4, DT_BF16>(a, idx, T, top_k, x_per_expert, experts, xs, ys);
+    return a.sb_dtype == DT_F16 ? gather_mt<8, DT_F16>(a, idx, T, top_k, x_per_expert, experts, xs, ys)
+                                : gather_mt<8, DT_BF16>(a, idx, T, top_k, x_per_expert, experts, xs, ys);
+}
 
 }  // namespace miqmm

@@ -21,6 +21,7 @@ raises.  torch provides device memory and the current HIP stream only.
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 from typing import Optional
 
@@ -77,6 +78,7 @@ def lib() -> ctypes.CDLL:
     L.miqmm_query_route.argtypes = [I64, I64, I64, I, I, ctypes.POINTER(I), ctypes.POINTER(I)]
     L.miqmm_synth_problem.argtypes = [P, P, P, P, I64, I64, I64, I, I, I, I, U64, U64, P]
     L.miqmm_quantized_matmul_grouped.argtypes = [ctypes.POINTER(Problem), I, I64, I64, I, I, I, I, I, P]
+    L.miqmm_gather_qmm.argtypes = [P, P, P, P, P, P, I64, I64, I, I64, I64, I64, I64, I, I, I, I, I, I, I, P]
     for name in ("miqmm_quantized_matmul", "miqmm_quantized_matmul_ex", "miqmm_quantized_linear",
                  "miqmm_dequantize", "miqmm_unpack", "miqmm_query_route", "miqmm_synth_problem",
                  "miqmm_quantized_matmul_grouped"):
@@ -212,6 +214,66 @@ def quantized_matmul_grouped(xs, ws, scales, biases, group_size: int = 64, bits:
     _check(lib().miqmm_quantized_matmul_grouped(probs, n, M, K, group_size, bits, _dt(xs[0].contiguous()),
                                                 _dt(scales[0]), _dt(outs[0]), _stream(stream)))
     return outs
+
+
+def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               rhs_indices: torch.Tensor, transpose: bool = True, group_size: int = 64, bits: int = 4,
+               sorted_indices: bool = False, *, out: Optional[torch.Tensor] = None,
+               stream=None) -> torch.Tensor:
+    """out[b] = x[b] @ dequant(w[rhs_indices[b]]).T over the broadcast batch b.
+
+    Argument order and meaning follow the reference's gather_qmm wrapper
+    (src/engine/mlx_lm/utils/moe.rs:33-43; lhs_indices absent): w is the
+    stacked experts [E, N, K*bits/32], scales/biases [E, N, K/group_size],
+    x [..., M, K] whose batch dims broadcast against rhs_indices [...];
+    the result is [*broadcast, M, N].  An index outside [0, E) gives zero rows.
+    sorted_indices is a hint that changes nothing here."""
+    if w.dim() != 3 or scales.dim() != 3 or biases.shape != scales.shape or scales.shape[0] != w.shape[0]:
+        raise MiqmmError(EINVAL, f"w {tuple(w.shape)} and scales/biases {tuple(scales.shape)}/"
+                                 f"{tuple(biases.shape)} must be stacked [E, N, ...] with equal shapes")
+    E = w.shape[0]
+    if E == 0:
+        raise MiqmmError(EINVAL, "w holds no experts")
+    N, K = _check_weights(w[0], scales[0], biases[0], group_size, bits)
+    if x.dim() < 2 or x.shape[-1] != K:
+        raise MiqmmError(EINVAL, f"x {tuple(x.shape)} must be [..., M, {K}]")
+    if rhs_indices.dtype.is_floating_point or rhs_indices.dtype == torch.bool:
+        raise MiqmmError(EINVAL, f"rhs_indices must hold integers, got {rhs_indices.dtype}")
+    M = x.shape[-2]
+    try:
+        bshape = tuple(torch.broadcast_shapes(tuple(x.shape[:-2]), tuple(rhs_indices.shape)))
+    except RuntimeError as e:
+        raise MiqmmError(EINVAL, f"x batch {tuple(x.shape[:-2])} does not broadcast against "
+                                 f"rhs_indices {tuple(rhs_indices.shape)}") from e
+    idx = rhs_indices.expand(bshape).to(torch.int32).contiguous()
+    # x shared by a trailing block of the batch (x [..., 1, 1, M, K] against
+    # indices [..., top_k]) is passed once per leading batch entry; any other
+    # broadcast is materialised, one x matrix per selection
+    xb = (1,) * (len(bshape) - (x.dim() - 2)) + tuple(x.shape[:-2])
+    j = len(bshape)
+    while j > 0 and xb[j - 1] == 1:
+        j -= 1
+    if xb[:j] == bshape[:j]:
+        batch = math.prod(bshape[:j])
+        top_k = math.prod(bshape[j:])
+        xc = x.contiguous()
+        per_index = 0
+    else:
+        batch, top_k = math.prod(bshape), 1
+        xc = x.expand(bshape + (M, K)).contiguous()
+        per_index = 1
+    if top_k == 1:
+        per_index = 1
+    ydt = result_type(x.dtype, scales.dtype)
+    shape = bshape + (M, N)
+    if out is None:
+        out = torch.empty(shape, dtype=ydt, device=x.device)
+    elif out.shape != shape or not out.is_contiguous() or out.dtype != ydt:
+        raise MiqmmError(EINVAL, f"out must be contiguous {shape} of {ydt}")
+    _check(lib().miqmm_gather_qmm(_ptr(out), _ptr(xc), _ptr(w), _ptr(scales), _ptr(biases), _ptr(idx), batch,
+                                  top_k, per_index, M, N, K, E, int(bool(transpose)), group_size, bits, _dt(xc),
+                                  _dt(scales), _dt(out), int(bool(sorted_indices)), _stream(stream)))
+    return out
 
 
 def quantized_linear(x, w, scales, biases, bias=None, group_size: int = 64, bits: int = 4, **kw):

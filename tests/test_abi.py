@@ -103,6 +103,47 @@ def test_grouped_entry_point_validates(lib):
     assert G(probs, 2, 0, 128, 64, 4, 0, 0, 0, None) == miqmm.OK      # M == 0 is a no-op
 
 
+def test_gather_entry_point_validates(lib):
+    import miqmm
+
+    P = ctypes.c_void_p(16)
+
+    def G(idx=P, batch=1, top_k=6, xpi=0, M=1, N=64, K=128, E=8, transpose=1, g=64, bits=4, y=P):
+        return lib.miqmm_gather_qmm(y, P, P, P, P, idx, batch, top_k, xpi, M, N, K, E, transpose, g, bits,
+                                    0, 0, 0, 0, None)
+
+    assert G(batch=-1) == miqmm.EINVAL and "batch and top_k" in lib.miqmm_last_error().decode()
+    assert G(E=0) == miqmm.EINVAL and "experts" in lib.miqmm_last_error().decode()
+    assert G(xpi=2) == miqmm.EINVAL
+    assert G(transpose=0) == miqmm.ENOTSUP
+    assert G(bits=3) == miqmm.ENOTSUP
+    assert G(K=96) == miqmm.EINVAL
+    assert G(idx=None) == miqmm.EINVAL and "null" in lib.miqmm_last_error().decode()
+    assert G(y=None) == miqmm.EINVAL
+    # no selections or no rows: nothing is read, so null pointers are accepted
+    assert G(batch=0, idx=None, y=None) == miqmm.OK
+    assert G(M=0, idx=None, y=None) == miqmm.OK
+
+
+def test_gather_python_shape_checks(lib):
+    import torch
+
+    import miqmm
+
+    w = torch.zeros((4, 8, 16), dtype=torch.int32)
+    s = torch.zeros((4, 8, 2), dtype=torch.bfloat16)
+    x = torch.zeros((2, 1, 1, 128), dtype=torch.bfloat16)
+    idx = torch.zeros((2, 3), dtype=torch.int32)
+    with pytest.raises(miqmm.MiqmmError, match="stacked"):
+        miqmm.gather_qmm(x, w[0], s[0], s[0], idx)
+    with pytest.raises(miqmm.MiqmmError, match="must be"):
+        miqmm.gather_qmm(x[..., :64], w, s, s, idx)
+    with pytest.raises(miqmm.MiqmmError, match="broadcast"):
+        miqmm.gather_qmm(x, w, s, s, torch.zeros((3, 3), dtype=torch.int32))
+    with pytest.raises(miqmm.MiqmmError, match="integers"):
+        miqmm.gather_qmm(x, w, s, s, idx.float())
+
+
 def test_query_route(lib):
     import miqmm
 

@@ -256,3 +256,95 @@ def test_pins_reject_planted_mistakes(c_oracle):
     assert not np.allclose(xf @ (sf_bad * q + bf).T, good, atol=1e-3)
     # a wrong sign on the bias fails too
     assert not np.allclose(xf @ (sf * q - bf).T, good, atol=1e-3)
+
+
+# ------------------------------------------------------------------ gather_qmm
+def _experts(E, N, K, g, bits, seed):
+    ws, ss, bs = [], [], []
+    for e in range(E):
+        _, w, s, b = O.synth_problem(1, N, K, g, bits, seed=seed, stream=100 + e)
+        ws.append(w), ss.append(s), bs.append(b)
+    return np.stack(ws), np.stack(ss), np.stack(bs)
+
+
+def _brute_gather(x, w, s, b, idx, K, g, bits):
+    # independent restatement: scalar loops, codes read bit by bit from the words
+    E, N = w.shape[0], w.shape[1]
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    sf = O.bf16_to_f32(s).astype(np.float64)
+    bf = O.bf16_to_f32(b).astype(np.float64)
+    per = 32 // bits
+    out = np.zeros(idx.shape + (x.shape[-2], N))
+    for pos in np.ndindex(*idx.shape):
+        e = int(idx[pos])
+        xm = xf[pos[0]] if xf.ndim == 3 else xf[pos]
+        if not 0 <= e < E:
+            continue
+        for m in range(xm.shape[0]):
+            for n in range(N):
+                acc = 0.0
+                for k in range(K):
+                    word = int(w[e, n, k // per])
+                    q = (word >> (bits * (k % per))) & ((1 << bits) - 1)
+                    acc += xm[m, k] * (sf[e, n, k // g] * q + bf[e, n, k // g])
+                out[pos + (m, n)] = acc
+    return out
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_brute_force(bits):
+    E, N, K, g, M = 3, 5, 64, 32, 2
+    w, s, b = _experts(E, N, K, g, bits, seed=11)
+    x, _, _, _ = O.synth_problem(2 * M, N, K, g, bits, seed=12)
+    x = x.reshape(2, M, K)
+    idx = np.array([[2, 0, 1], [1, 1, -1]], np.int64)  # [batch 2, top_k 3]; -1 is out of range
+    got = O.gather_qmm_f64(x[:, None], w, s, b, idx, K, g, bits)
+    assert got.shape == (2, 3, M, N)
+    want = _brute_gather(x, w, s, b, idx, K, g, bits)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    assert not got[1, 2].any()
+
+
+def test_gather_reference_test_shape():
+    # the reference's test geometry (moe.rs:84-146): E=4, out=32, in=64, g=64,
+    # bits=4, x [3, 1, 1, 64] against inds [3, 2] = [0,1,2,3,1,0] -> [3, 2, 1, 32],
+    # each slice equal to dequantize(w[e]) @ x[m]
+    E, N, K, g, bits = 4, 32, 64, 64, 4
+    w, s, b = _experts(E, N, K, g, bits, seed=5)
+    x, _, _, _ = O.synth_problem(3, N, K, g, bits, seed=6)
+    inds = np.array([0, 1, 2, 3, 1, 0]).reshape(3, 2)
+    got = O.gather_qmm_f64(x.reshape(3, 1, 1, K), w, s, b, inds, K, g, bits)
+    assert got.shape == (3, 2, 1, N)
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    for mi in range(3):
+        for ki in range(2):
+            e = inds[mi, ki]
+            wd = O.dequantize(w[e], s[e], b[e], K, g, bits, exact=True)
+            np.testing.assert_allclose(got[mi, ki, 0], wd @ xf[mi], rtol=1e-12, atol=1e-12)
+
+
+def test_gather_constant_index_is_quantized_matmul():
+    E, N, K, g, bits, M = 4, 16, 128, 64, 4, 3
+    w, s, b = _experts(E, N, K, g, bits, seed=7)
+    x, _, _, _ = O.synth_problem(M, N, K, g, bits, seed=8)
+    for e in range(E):
+        got = O.gather_qmm_f64(x, w, s, b, np.full((5,), e), K, g, bits)
+        want = O.qmm_f64(x, w[e], s[e], b[e], K, g, bits)
+        for i in range(5):
+            np.testing.assert_array_equal(got[i], want)
+
+
+def test_gather_pins_reject_planted_mistakes():
+    # an index read transposed ([top_k, batch] order) or an x taken per
+    # selection instead of per token changes the brute-force result
+    E, N, K, g, bits, M = 3, 4, 32, 32, 4, 1
+    w, s, b = _experts(E, N, K, g, bits, seed=9)
+    x, _, _, _ = O.synth_problem(2 * M, N, K, g, bits, seed=10)
+    x = x.reshape(2, M, K)
+    idx = np.array([[0, 1, 2], [2, 2, 0]])
+    want = _brute_gather(x, w, s, b, idx, K, g, bits)
+    bad_t = O.gather_qmm_f64(x[:, None], w, s, b, idx.T.reshape(2, 3), K, g, bits)
+    assert not np.allclose(bad_t, want, atol=1e-3)
+    bad_x = O.gather_qmm_f64(x[::-1].copy()[:, None], w, s, b, idx, K, g, bits)
+    assert not np.allclose(bad_x, want, atol=1e-3)
+    np.testing.assert_allclose(O.gather_qmm_f64(x[:, None], w, s, b, idx, K, g, bits), want, rtol=1e-12)
