@@ -74,6 +74,41 @@ __device__ __forceinline__ void store_out(void* y, int64_t idx, int y_dtype, flo
     }
 }
 
+// R consecutive outputs y[base + n0 .. base + n0 + R) of one output row (each
+// as store_out would write it), stored by the calling lane as one vector store
+// when all R lie below N and the address allows it, else one by one.  A GEMV
+// tile's rows are adjacent in y, so this replaces R partial-line stores from R
+// lanes with one.
+template <int R>
+__device__ __forceinline__ void store_run(void* y, int64_t base, int n0, int N, int y_dtype, const float (&v)[R],
+                                          const void* bias) {
+    using u32x2_t = uint32_t __attribute__((ext_vector_type(2)));
+    if (y_dtype == DT_F32) {
+        float* p = (float*)y + base + n0;
+        if (R >= 2 && n0 + R <= N && (reinterpret_cast<uintptr_t>(p) & (4 * R - 1)) == 0) {
+            uint32_t o[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) o[r] = __float_as_uint(bias ? v[r] + ((const float*)bias)[n0 + r] : v[r]);
+            if constexpr (R == 4) *reinterpret_cast<u32x4_t*>(p) = u32x4_t{o[0], o[1], o[2], o[3]};
+            else if constexpr (R == 2) *reinterpret_cast<u32x2_t*>(p) = u32x2_t{o[0], o[1]};
+            return;
+        }
+    } else {
+        uint16_t* p = (uint16_t*)y + base + n0;
+        if (R >= 2 && n0 + R <= N && (reinterpret_cast<uintptr_t>(p) & (2 * R - 1)) == 0) {
+            uint32_t h[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) h[r] = out_half_bits(y_dtype, v[r], bias, n0 + r);
+            if constexpr (R == 4) *reinterpret_cast<u32x2_t*>(p) = u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+            else if constexpr (R == 2) *reinterpret_cast<uint32_t*>(p) = h[0] | (h[1] << 16);
+            return;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (n0 + r < N) store_out(y, base + n0 + r, y_dtype, v[r], bias, n0 + r);
+}
+
 // ---------------------------------------------------------------- bit tricks
 // bf16 with bits 0x4300|q is exactly 128+q for q < 128: a 4-bit code becomes
 // an exact bf16 operand with one and-or.  Pairs are (q_j, q_{j+4}) of a word.

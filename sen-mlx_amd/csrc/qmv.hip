@@ -240,16 +240,19 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
             const int row0 = tc.row0 + sg * R;
             j_c = 0;
             tile_c += nwaves;
+            float v[MT][R];
 #pragma unroll
             for (int r = 0; r < R; ++r)
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
-                    const float v = lane_group_sum<L>(acc[r][m]);
+                    v[m][r] = lane_group_sum<L>(acc[r][m]);
                     acc[r][m] = 0.f;
-                    const int n = row0 + r;
-                    if (li == L - 16 + ((r * MT + m) & 15) && m < M && n < N)
-                        store_out(y, (int64_t)m * N + n, y_dtype, v, bias, n);
                 }
+            if (li == L - 1) {  // holds every sum of its sub-group: one store per row of x
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    if (m < M) store_run<R>(y, (int64_t)m * N, row0, N, y_dtype, v[m], bias);
+            }
         }
     };
 
@@ -342,8 +345,20 @@ int pick_l(int64_t K, int bits) {
     return best;
 }
 
-// rows per sub-group: fewer as M grows (registers for x and accumulators)
-int pick_r(int64_t M) { return M <= 2 ? 4 : M <= 4 ? 2 : 1; }
+// rows per sub-group.  More rows amortise the lane reduction and the x chunk
+// (M <= 2 affords 4, M <= 4 two, more rows of x one, for registers), but a
+// small N then leaves most of the chip idle and the launch latency-bound: take
+// the largest R that still gives kFillTiles row tiles, else 1 (measured on
+// MI355X, 4-bit g64, M = 1: N = 896 runs 2.60 -> 2.16 us with R = 1, N = 9728
+// 4.12 -> 3.80 us with R = 2, N = 14336 at K = 4096 is best at R = 4).
+constexpr int64_t kFillTiles = 1536;
+int pick_r(int64_t M, int64_t rows, int L) {
+    const int rmax = M <= 2 ? 4 : M <= 4 ? 2 : 1;
+    const int64_t sg = 64 / L;
+    for (int r = rmax; r > 1; r /= 2)
+        if ((rows + sg * r - 1) / (sg * r) >= kFillTiles) return r;
+    return 1;
+}
 
 template <int BITS, int SBT, int MT, int R>
 hipError_t launch_l(const QmmArgs* a, int count) {
@@ -354,21 +369,37 @@ hipError_t launch_l(const QmmArgs* a, int count) {
     }
 }
 
+template <int BITS, int SBT, int MT>
+hipError_t launch_r(const QmmArgs* a, int count, int r) {
+    if constexpr (MT <= 2) {
+        if (r == 4) return launch_l<BITS, SBT, MT, 4>(a, count);
+        if (r == 2) return launch_l<BITS, SBT, MT, 2>(a, count);
+        return launch_l<BITS, SBT, MT, 1>(a, count);
+    } else if constexpr (MT == 4) {
+        return launch_l<BITS, SBT, MT, 2>(a, count);
+    } else {
+        return launch_l<BITS, SBT, MT, 1>(a, count);
+    }
+}
+
 template <int BITS, int SBT>
 hipError_t launch_mt(const QmmArgs* a, int count) {
+    int64_t rows = 0;
+    for (int i = 0; i < count; ++i) rows += a[i].N;
+    const int r = pick_r(a[0].M, rows, pick_l(a[0].K, a[0].bits));
     switch (pick_mt(a[0].M)) {
-        case 1: return launch_l<BITS, SBT, 1, 4>(a, count);
-        case 2: return launch_l<BITS, SBT, 2, 4>(a, count);
-        case 4: return launch_l<BITS, SBT, 4, 2>(a, count);
-        case 8: return launch_l<BITS, SBT, 8, 1>(a, count);
-        default: return launch_l<BITS, SBT, 16, 1>(a, count);
+        case 1: return launch_r<BITS, SBT, 1>(a, count, r);
+        case 2: return launch_r<BITS, SBT, 2>(a, count, r);
+        case 4: return launch_r<BITS, SBT, 4>(a, count, r);
+        case 8: return launch_r<BITS, SBT, 8>(a, count, r);
+        default: return launch_r<BITS, SBT, 16>(a, count, r);
     }
 }
 
 }  // namespace
 
 void qmv_config(const QmmArgs& a, int* rows_per_subgroup, int* m_tile, int* lanes_per_row) {
-    if (rows_per_subgroup) *rows_per_subgroup = pick_r(a.M);
+    if (rows_per_subgroup) *rows_per_subgroup = pick_r(a.M, a.N, pick_l(a.K, a.bits));
     if (m_tile) *m_tile = pick_mt(a.M);
     if (lanes_per_row) *lanes_per_row = pick_l(a.K, a.bits);
 }
@@ -395,9 +426,16 @@ hipError_t gather_l(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, 
 template <int BITS, int SBT>
 hipError_t gather_mt(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int xpe, int64_t E, int64_t xs,
                      int64_t ys) {
+    const int r = pick_r(a.M, a.N * T * top_k, pick_l(a.K, a.bits));
     switch (pick_mt(a.M)) {
-        case 1: return gather_l<BITS, SBT, 1, 4>(a, idx, T, top_k, xpe, E, xs, ys);
-        case 2: return gather_l<BITS, SBT, 2, 4>(a, idx, T, top_k, xpe, E, xs, ys);
+        case 1:
+            return r == 4   ? gather_l<BITS, SBT, 1, 4>(a, idx, T, top_k, xpe, E, xs, ys)
+                   : r == 2 ? gather_l<BITS, SBT, 1, 2>(a, idx, T, top_k, xpe, E, xs, ys)
+                            : gather_l<BITS, SBT, 1, 1>(a, idx, T, top_k, xpe, E, xs, ys);
+        case 2:
+            return r == 4   ? gather_l<BITS, SBT, 2, 4>(a, idx, T, top_k, xpe, E, xs, ys)
+                   : r == 2 ? gather_l<BITS, SBT, 2, 2>(a, idx, T, top_k, xpe, E, xs, ys)
+                            : gather_l<BITS, SBT, 2, 1>(a, idx, T, top_k, xpe, E, xs, ys);
         case 4: return gather_l<BITS, SBT, 4, 2>(a, idx, T, top_k, xpe, E, xs, ys);
         case 8: return gather_l<BITS, SBT, 8, 1>(a, idx, T, top_k, xpe, E, xs, ys);
         default: return gather_l<BITS, SBT, 16, 1>(a, idx, T, top_k, xpe, E, xs, ys);
