@@ -94,8 +94,10 @@ typedef struct miqmm_problem {
  * in the reference: it replaces the reference's separate quantized projections
  * that read the same activation -- q/k/v (src/engine/mlx_lm/models/llama.rs:
  * 195-197) and gate/up (:293-294) -- whose decode-step launches are otherwise
- * latency-bound.  Each problem's result equals miqmm_quantized_matmul (or
- * miqmm_quantized_linear when bias is set) on it alone.
+ * latency-bound.  In the grouped case each problem's result equals, bit for
+ * bit, miqmm_quantized_matmul_ex with MIQMM_ROUTE_QMV_DOT on it alone (plus
+ * the bias as miqmm_quantized_linear adds it); otherwise it equals
+ * miqmm_quantized_matmul (or miqmm_quantized_linear) on it alone.
  */
 int miqmm_quantized_matmul_grouped(const miqmm_problem* problems, int count, int64_t M, int64_t K,
                                    int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,

@@ -190,16 +190,28 @@ int miqmm_quantized_matmul_grouped(const miqmm_problem* problems, int count, int
         }
         return ok();
     }
-    for (int i0 = 0; i0 < count; i0 += miqmm::kMaxGroup) {
-        miqmm::QmmArgs a[miqmm::kMaxGroup];
-        const int n = count - i0 < miqmm::kMaxGroup ? count - i0 : miqmm::kMaxGroup;
-        for (int i = 0; i < n; ++i) {
-            const miqmm_problem& p = problems[i0 + i];
-            a[i] = miqmm::QmmArgs{p.y, p.x, p.w, p.scales, p.biases, p.bias, M, p.N, K, group_size, bits,
-                                  x_dtype, sb_dtype, y_dtype, reinterpret_cast<hipStream_t>(stream)};
+    // a problem that the GEMV alone would run with K split over a block's
+    // waves is launched alone, so that every result equals the v_dot2 route
+    // on that problem bit for bit (the split changes the order of the sums)
+    miqmm::QmmArgs a[miqmm::kMaxGroup];
+    int n = 0;
+    for (int i = 0; i <= count; ++i) {
+        if (i < count) {
+            const miqmm_problem& p = problems[i];
+            const miqmm::QmmArgs q{p.y, p.x, p.w, p.scales, p.biases, p.bias, M, p.N, K, group_size, bits,
+                                   x_dtype, sb_dtype, y_dtype, reinterpret_cast<hipStream_t>(stream)};
+            if (miqmm::qmv_ksplit(M, p.N, K, bits)) {
+                const int st = check_launch(miqmm::launch_qmv(q), "qmv_dot launch");
+                if (st != MIQMM_OK) return st;
+                continue;
+            }
+            a[n++] = q;
         }
-        const int st = check_launch(miqmm::launch_qmv_grouped(a, n), "grouped qmv_dot launch");
-        if (st != MIQMM_OK) return st;
+        if (n == miqmm::kMaxGroup || (i == count && n > 0)) {
+            const int st = check_launch(miqmm::launch_qmv_grouped(a, n), "grouped qmv_dot launch");
+            if (st != MIQMM_OK) return st;
+            n = 0;
+        }
     }
     return ok();
 }

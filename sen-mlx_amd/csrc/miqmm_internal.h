@@ -42,11 +42,17 @@ struct GemvProblems {
     const int32_t* idx;
     int top_k, x_per_expert, experts, tiles_per_problem;
     int64_t x_stride, y_stride;  // elements between consecutive x / y matrices
+    // 1: the 4 waves of a block share each row tile, wave w taking the w-th
+    // quarter of its chunks, and add their partial sums through LDS
+    int ksplit;
 };
 
 // route launchers; return hipSuccess or the launch error
 hipError_t launch_qmv(const QmmArgs& a);       // VALU dot2 GEMV
 hipError_t launch_qmv_grouped(const QmmArgs* a, int count);  // same, count <= kMaxGroup problems
+// whether launch_qmv on this shape alone splits K over a block's waves (a
+// grouped launch never does, so such problems are launched on their own)
+bool qmv_ksplit(int64_t M, int64_t N, int64_t K, int bits);
 // expert-gathered GEMVs: a describes one expert (w/scales/biases = expert 0 of
 // the stack), x holds T*(x_per_expert ? top_k : 1) matrices, y holds T*top_k
 // matrices of N columns, x_stride / y_stride elements apart; a.M <= 16 rows of

@@ -34,6 +34,7 @@ namespace {
 
 constexpr int kMaxBlocksPerCU = 8;
 constexpr int kNumCUs = 256;
+constexpr int64_t kFillTiles = 1536;  // row tiles that keep the chip busy (see pick_r)
 
 // one pipeline stage: the codes, scales and biases of R rows at one chunk
 // position, and (when XPF) the matching x chunk of every row of x
@@ -50,6 +51,16 @@ struct Stage {
 // rather than an index, which would copy the table to scratch
 __device__ __forceinline__ const GemvProblem& pick4(const GemvProblems& P, int p) {
     return p == 0 ? P.p[0] : p == 1 ? P.p[1] : p == 2 ? P.p[2] : P.p[3];
+}
+
+// block barrier over LDS written with ds_write: lgkmcnt(0), then s_barrier,
+// fenced against compiler reordering (__syncthreads() would also wait for
+// every buffer load in flight)
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 // where one row tile of the grid reads and writes
@@ -93,9 +104,18 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
         }
         return p;
     };
-    const int my_tiles = gwave < tiles ? (tiles - 1 - gwave) / nwaves + 1 : 0;
-    const int iters = my_tiles * J;
-    if (iters == 0) return;  // wave-uniform
+    // tiles and chunk iterations of this wave: its own tiles over all J chunk
+    // passes, or with ksplit the block's tiles over this wave's quarter of them
+    const int wv = threadIdx.x >> 6;
+    const bool ks = P.ksplit != 0;
+    const int tile_first = ks ? (int)blockIdx.x : gwave;
+    const int tile_stride = ks ? (int)gridDim.x : nwaves;
+    const int j_begin = ks ? wv * J / 4 : 0;
+    const int j_count = ks ? (wv + 1) * J / 4 - j_begin : J;
+    const int my_tiles = tile_first < tiles ? (tiles - 1 - tile_first) / tile_stride + 1 : 0;
+    const int iters = my_tiles * j_count;
+    if (iters == 0) return;  // uniform over the block when ksplit (J >= 4 gives every wave chunks)
+    __shared__ float kpart[2][4][64];  // ksplit partial sums, double-buffered by tile parity
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
     const int ysz = y_dtype == DT_F32 ? 4 : 2;
@@ -169,13 +189,13 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     };
 
     // (tile, chunk iteration) of the next stage to issue and of the stage being computed
-    int tile_i = gwave, j_i = 0, tile_c = gwave, j_c = 0;
+    int tile_i = tile_first, j_i = 0, tile_c = tile_first, j_c = 0, k_c = 0;
     auto issue = [&](St& st) {
         const int tile = tile_i;
-        const int c = li + j_i * L;
-        if (++j_i == J) {
+        const int c = li + (j_begin + j_i) * L;
+        if (++j_i == j_count) {
             j_i = 0;
-            tile_i += nwaves;
+            tile_i += tile_stride;
         }
         const TileRef t = locate(tile);
         const uint32_t valid_rows = (uint32_t)t.rows;
@@ -232,14 +252,14 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
                 acc[r][m] = fmaf(b, xs[m], acc[r][m]);
             }
         }
-        if (++j_c == J) {  // tile complete: reduce over the sub-group and store
+        if (++j_c == j_count) {  // tile complete: reduce over the sub-group and store
             const TileRef tc = locate(tile_c);
             const int N = tc.N;
             void* const y = tc.y;
             const void* const bias = tc.bias;
             const int row0 = tc.row0 + sg * R;
             j_c = 0;
-            tile_c += nwaves;
+            tile_c += tile_stride;
             float v[MT][R];
 #pragma unroll
             for (int r = 0; r < R; ++r)
@@ -248,7 +268,29 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
                     v[m][r] = lane_group_sum<L>(acc[r][m]);
                     acc[r][m] = 0.f;
                 }
-            if (li == L - 1) {  // holds every sum of its sub-group: one store per row of x
+            bool owner = true;
+            if (ks) {  // the block's four partials of this tile meet in LDS; wave 0 stores
+                float* const kp = kpart[k_c & 1][0];
+                if (li == L - 1) {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) kp[wv * 64 + (sg * MT + m) * R + r] = v[m][r];
+                }
+                lds_barrier();
+                owner = wv == 0;
+                if (owner && li == L - 1) {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            const int o = (sg * MT + m) * R + r;
+                            v[m][r] = (kp[o] + kp[64 + o]) + (kp[128 + o] + kp[192 + o]);
+                        }
+                }
+                ++k_c;
+            }
+            if (owner && li == L - 1) {  // holds every sum of its sub-group: one store per row of x
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
                     if (m < M) store_run<R>(y, (int64_t)m * N, row0, N, y_dtype, v[m], bias);
@@ -270,6 +312,21 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     }
 }
 
+// Too few row tiles to fill the chip even at one row per sub-group, and rows
+// long enough (J >= 4 chunk passes) to split: the four waves of a block
+// share each tile, each streaming a quarter of its chunks.
+int use_ksplit(int64_t tiles, int64_t K, int bits, int L) {
+    const int64_t J = (K * bits / 128 + L - 1) / L;
+    return J >= 4 && tiles < kFillTiles ? 1 : 0;
+}
+
+// blocks of 4 waves: one tile per wave (or per block when split), at most
+// kMaxBlocksPerCU blocks per CU, the waves then walking further tiles
+int gemv_blocks(int64_t tiles, int ksplit) {
+    const int64_t want = ksplit ? tiles : (tiles + 3) / 4;
+    return (int)(want < kNumCUs * kMaxBlocksPerCU ? want : kNumCUs * kMaxBlocksPerCU);
+}
+
 // a[0..count) share M, K, group size, bits and dtypes; one grid covers all
 // (grouped grids are built for one or two rows of x only)
 template <int BITS, int SBT, int MT, int L, int R>
@@ -285,8 +342,8 @@ hipError_t launch_t(const QmmArgs* a, int count) {
         if (i < count) tiles += (q.N + TILE - 1) / TILE;
     }
     P.tiles = (int)tiles;
-    const int64_t want = (tiles + 3) / 4;
-    const int blocks = (int)(want < kNumCUs * kMaxBlocksPerCU ? want : kNumCUs * kMaxBlocksPerCU);
+    P.ksplit = use_ksplit(tiles, a[0].K, a[0].bits, L);
+    const int blocks = gemv_blocks(tiles, P.ksplit);
     const int gs_shift = __builtin_ctz((unsigned)a[0].group_size);
     if constexpr (MT <= 2) {
         if (count > 1) {
@@ -318,8 +375,8 @@ hipError_t launch_gather_t(const QmmArgs& a, const int32_t* idx, int64_t T, int 
     const int64_t tiles = (int64_t)P.tiles_per_problem * T * top_k;
     if (tiles >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
     P.tiles = (int)tiles;
-    const int64_t want = (tiles + 3) / 4;
-    const int blocks = (int)(want < kNumCUs * kMaxBlocksPerCU ? want : kNumCUs * kMaxBlocksPerCU);
+    P.ksplit = use_ksplit(tiles, a.K, a.bits, L);
+    const int blocks = gemv_blocks(tiles, P.ksplit);
     const int gs_shift = __builtin_ctz((unsigned)a.group_size);
     hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 2>), dim3(blocks), dim3(256), 0, a.stream, P, (int)a.M,
                        (int)a.K, gs_shift, a.y_dtype);
@@ -351,7 +408,6 @@ int pick_l(int64_t K, int bits) {
 // the largest R that still gives kFillTiles row tiles, else 1 (measured on
 // MI355X, 4-bit g64, M = 1: N = 896 runs 2.60 -> 2.16 us with R = 1, N = 9728
 // 4.12 -> 3.80 us with R = 2, N = 14336 at K = 4096 is best at R = 4).
-constexpr int64_t kFillTiles = 1536;
 int pick_r(int64_t M, int64_t rows, int L) {
     const int rmax = M <= 2 ? 4 : M <= 4 ? 2 : 1;
     const int64_t sg = 64 / L;
@@ -397,6 +453,12 @@ hipError_t launch_mt(const QmmArgs* a, int count) {
 }
 
 }  // namespace
+
+bool qmv_ksplit(int64_t M, int64_t N, int64_t K, int bits) {
+    const int L = pick_l(K, bits);
+    const int64_t tile = (64 / L) * pick_r(M, N, L);
+    return use_ksplit((N + tile - 1) / tile, K, bits, L) != 0;
+}
 
 void qmv_config(const QmmArgs& a, int* rows_per_subgroup, int* m_tile, int* lanes_per_row) {
     if (rows_per_subgroup) *rows_per_subgroup = pick_r(a.M, a.N, pick_l(a.K, a.bits));
