@@ -157,6 +157,20 @@ int miqmm_dequantize(void* out, const uint32_t* w, const void* scales, const voi
                      void* stream);
 
 /*
+ * Quantized embedding lookup: out[t, k] = scales[id,k/g] * q[id,k] +
+ * biases[id,k/g] (fp32 fma, stored as out_dtype) with id = ids[t], for
+ * t < T, from a table of V rows of K codes (w [V, K*bits/32], scales and
+ * biases [V, K/g]).  An id outside [0, V) gives a zero row.  ids: int32 on
+ * the device.  Replaces QuantizedEmbedding::forward as the reference
+ * restates it (src/engine/mlx_lm/models/bonsai_q1.rs:603-613: take the rows,
+ * then mlx dequantize), the step before the first projection of every token;
+ * the table is the one loaded at src/engine/mlx_native.rs:3532-3560,3712-3731.
+ */
+int miqmm_quantized_embedding(void* out, const int32_t* ids, int64_t T, const uint32_t* w, const void* scales,
+                              const void* biases, int64_t V, int64_t K, int group_size, int bits, int sb_dtype,
+                              int out_dtype, void* stream);
+
+/*
  * codes[n*K + k] = q[n, k] (uint8): the kernels' unpacking convention,
  * exposed so it can be checked bit-exactly against the packed layout of
  * src/engine/mlx_lm/models/bonsai_q1.rs:137-143 (bits=1), generalised.

@@ -11,6 +11,7 @@ Reference citations (SenClaw/sen-mlx tree):
     (bits=1), generalised to bits 4 and 8.
   - shapes w [N, K*bits/32], scales/biases [N, K/g]: src/engine/mlx_lm/utils/moe.rs:20-31.
   - dequant fma(scale, q, bias) in fp32: src/engine/mlx_lm/models/bonsai_q1.rs:172.
+  - quantized embedding lookup: src/engine/mlx_lm/models/bonsai_q1.rs:603-613.
   - gather_qmm (stacked experts [E, N, ...] selected per batch entry):
     src/engine/mlx_lm/utils/moe.rs:20-31, test at moe.rs:84-146.
 
@@ -159,6 +160,24 @@ def dequantize(w, s, b, K, group_size, bits, sb_dtype=BF16, exact=False) -> np.n
 def qmm_f64(x, w, s, b, K, group_size, bits, x_dtype=BF16, sb_dtype=BF16) -> np.ndarray:
     wd = dequantize(w, s, b, K, group_size, bits, sb_dtype, exact=True)
     return half_to_f32(x, x_dtype).astype(np.float64) @ wd.T
+
+
+def embedding(ids, w, s, b, K, group_size, bits, sb_dtype=BF16, out_dtype=BF16) -> np.ndarray:
+    """out[..., k] = fma(s, q, b) of row ids[...] in fp32, rounded to out_dtype
+    (bit patterns for bf16/fp16, float32 values for F32); an id outside
+    [0, V) gives a zero row.  Restates the lookup at
+    src/engine/mlx_lm/models/bonsai_q1.rs:603-613 (take rows, then dequantize)."""
+    ids = np.asarray(ids)
+    V = w.shape[0]
+    flat = ids.reshape(-1).astype(np.int64)
+    ok = (flat >= 0) & (flat < V)
+    rows = np.where(ok, flat, 0)
+    d = dequantize(w[rows], s[rows], b[rows], K, group_size, bits, sb_dtype)  # fp32
+    d[~ok] = 0.0
+    d = d.reshape(ids.shape + (K,))
+    if out_dtype == F32:
+        return d.astype(np.float32)
+    return f32_to_half(d, out_dtype)
 
 
 def gather_qmm_f64(x, w, s, b, idx, K, group_size, bits, x_dtype=BF16, sb_dtype=BF16) -> np.ndarray:

@@ -262,6 +262,23 @@ int miqmm_dequantize(void* out, const uint32_t* w, const void* scales, const voi
                         "dequantize launch");
 }
 
+int miqmm_quantized_embedding(void* out, const int32_t* ids, int64_t T, const uint32_t* w, const void* scales,
+                              const void* biases, int64_t V, int64_t K, int group_size, int bits, int sb_dtype,
+                              int out_dtype, void* stream) {
+    int st = check_quant(V, K, group_size, bits, sb_dtype);
+    if (st != MIQMM_OK) return st;
+    if (out_dtype != MIQMM_DT_BF16 && out_dtype != MIQMM_DT_F16 && out_dtype != MIQMM_DT_F32)
+        return fail(MIQMM_EINVAL, "out dtype %d invalid", out_dtype);
+    if (T < 0 || T >= kMaxDim) return fail(MIQMM_EINVAL, "T must be in [0, 2^31), got %lld", (long long)T);
+    if (T == 0) return ok();
+    if (!out || !ids || !w || !scales || !biases) return fail(MIQMM_EINVAL, "null pointer argument");
+    if (!aligned16(w) || !aligned16(out)) return fail(MIQMM_EINVAL, "w and out must be 16-byte aligned");
+    if (T * K >= ((int64_t)1 << 40)) return fail(MIQMM_EINVAL, "T*K too large");
+    return check_launch(miqmm::launch_embedding(out, ids, T, w, scales, biases, V, K, group_size, bits, sb_dtype,
+                                                out_dtype, reinterpret_cast<hipStream_t>(stream)),
+                        "embedding launch");
+}
+
 int miqmm_unpack(uint8_t* codes, const uint32_t* w, int64_t N, int64_t K, int bits, void* stream) {
     if (bits != 4 && bits != 8) return fail(MIQMM_EINVAL, "bits must be 4 or 8, got %d", bits);
     if (N <= 0 || K <= 0 || K % 32 != 0) return fail(MIQMM_EINVAL, "need N > 0 and K > 0 with K %% 32 == 0");

@@ -6,6 +6,11 @@
 // (src/engine/mlx_lm/utils/moe.rs:118-126): out[n, k] = fma(s, q, b) in fp32
 // (src/engine/mlx_lm/models/bonsai_q1.rs:172), stored in the output dtype.
 //
+// embedding: MLX's QuantizedEmbedding lookup as the reference spells it out
+// (src/engine/mlx_lm/models/bonsai_q1.rs:603-613: take the selected rows of
+// the packed table, its scales and biases, then dequantize): out[t, k] =
+// fma(s, q, b) of row ids[t], in fp32, stored in the output dtype.
+//
 // synth: splitmix64 counter hash, draw i of stream (seed, tag) is
 // mix64(mix64(seed*G + tag) + i*G) with G = 0x9E3779B97F4A7C15; an
 // approximately N(0,1) value is the Irwin-Hall(4) sum of the draw's four
@@ -105,6 +110,53 @@ __global__ void dequantize_kernel(void* __restrict__ out, const uint32_t* __rest
     }
 }
 
+// One thread per 16-byte chunk of an output row (32 4-bit or 16 8-bit codes,
+// inside one group): consecutive threads read consecutive chunks of the
+// selected row and write consecutive 32/64-byte runs of the output.  An id
+// outside [0, V) gives a zero row (its chunk reads nothing).
+template <int BITS, int SBT>
+__global__ __launch_bounds__(256) void embedding_kernel(void* out, const int32_t* ids, int64_t T,
+                                                        const uint32_t* w, const uint16_t* sc, const uint16_t* bi,
+                                                        int64_t V, int64_t K, int gs_shift, int out_dtype) {
+    constexpr int CPC = 128 / BITS;  // codes per chunk
+    const int64_t C = K / CPC;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= T * C) return;
+    const int64_t t = i / C, c = i - t * C;
+    const int64_t id = ids[t];
+    const bool ok = id >= 0 && id < V;
+    const int64_t G = K >> gs_shift;
+    const int64_t g = (c * CPC) >> gs_shift;
+    const int64_t row = ok ? id : 0;
+    const u32x4_t q = ok ? *reinterpret_cast<const u32x4_t*>(w + (row * K + c * CPC) * BITS / 32) : u32x4_t{0, 0, 0, 0};
+    const float s = ok ? half_to_f32<SBT>(sc[row * G + g]) : 0.f;
+    const float b = ok ? half_to_f32<SBT>(bi[row * G + g]) : 0.f;
+    float v[CPC];
+#pragma unroll
+    for (int e = 0; e < CPC; ++e) {
+        const uint32_t code = (q[e * BITS / 32] >> ((e * BITS) & 31)) & ((1u << BITS) - 1u);
+        v[e] = f32_pinned(fmaf(s, (float)code, b));
+    }
+    const int64_t o = t * K + c * CPC;
+    if (out_dtype == DT_F32) {
+        u32x4_t* dst = reinterpret_cast<u32x4_t*>((float*)out + o);
+#pragma unroll
+        for (int e = 0; e < CPC / 4; ++e)
+            dst[e] = u32x4_t{__float_as_uint(v[4 * e]), __float_as_uint(v[4 * e + 1]), __float_as_uint(v[4 * e + 2]),
+                             __float_as_uint(v[4 * e + 3])};
+    } else {
+        u32x4_t* dst = reinterpret_cast<u32x4_t*>((uint16_t*)out + o);
+        const bool f16 = out_dtype == DT_F16;
+#pragma unroll
+        for (int e = 0; e < CPC / 8; ++e) {
+            uint32_t h[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) h[u] = f16 ? f32_to_f16_bits(v[8 * e + u]) : f32_to_bf16_bits(v[8 * e + u]);
+            dst[e] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+        }
+    }
+}
+
 __global__ void unpack_kernel(uint8_t* __restrict__ codes, const uint32_t* __restrict__ w, int64_t N,
                               int64_t K, int bits) {
     const int per = 32 / bits;
@@ -132,6 +184,32 @@ hipError_t launch_dequantize(void* out, const uint32_t* w, const void* scales, c
     else
         hipLaunchKernelGGL(dequantize_kernel<DT_BF16>, dim3(blocks_for(total, 256)), dim3(256), 0, stream,
                            out, w, (const uint16_t*)scales, (const uint16_t*)biases, N, K, gs_shift, bits, out_dtype);
+    return hipGetLastError();
+}
+
+hipError_t launch_embedding(void* out, const int32_t* ids, int64_t T, const uint32_t* w, const void* scales,
+                            const void* biases, int64_t V, int64_t K, int group_size, int bits, int sb_dtype,
+                            int out_dtype, hipStream_t stream) {
+    const int64_t total = T * (K * bits / 128);
+    const int gs_shift = __builtin_ctz((unsigned)group_size);
+    const auto* s16 = (const uint16_t*)scales;
+    const auto* b16 = (const uint16_t*)biases;
+    const dim3 grid(blocks_for(total, 256));
+    if (bits == 4) {
+        if (sb_dtype == DT_F16)
+            hipLaunchKernelGGL((embedding_kernel<4, DT_F16>), grid, dim3(256), 0, stream, out, ids, T, w, s16, b16, V,
+                               K, gs_shift, out_dtype);
+        else
+            hipLaunchKernelGGL((embedding_kernel<4, DT_BF16>), grid, dim3(256), 0, stream, out, ids, T, w, s16, b16,
+                               V, K, gs_shift, out_dtype);
+    } else {
+        if (sb_dtype == DT_F16)
+            hipLaunchKernelGGL((embedding_kernel<8, DT_F16>), grid, dim3(256), 0, stream, out, ids, T, w, s16, b16, V,
+                               K, gs_shift, out_dtype);
+        else
+            hipLaunchKernelGGL((embedding_kernel<8, DT_BF16>), grid, dim3(256), 0, stream, out, ids, T, w, s16, b16,
+                               V, K, gs_shift, out_dtype);
+    }
     return hipGetLastError();
 }
 

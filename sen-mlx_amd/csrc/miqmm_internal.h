@@ -73,6 +73,9 @@ void qmvx_config(const QmmArgs& a, int* m_tile, int* k_splits, int* stage_codes)
 hipError_t launch_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
                              int64_t N, int64_t K, int group_size, int bits, int sb_dtype,
                              int out_dtype, hipStream_t stream);
+hipError_t launch_embedding(void* out, const int32_t* ids, int64_t T, const uint32_t* w, const void* scales,
+                            const void* biases, int64_t V, int64_t K, int group_size, int bits, int sb_dtype,
+                            int out_dtype, hipStream_t stream);
 hipError_t launch_unpack(uint8_t* codes, const uint32_t* w, int64_t N, int64_t K, int bits,
                          hipStream_t stream);
 hipError_t launch_synth(void* x, uint32_t* w, void* scales, void* biases, int64_t M, int64_t N,

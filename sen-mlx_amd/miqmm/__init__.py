@@ -12,6 +12,11 @@ on its quantized decode/prefill path:
       forward = quantized_matmul, then + bias when the Linear had one (llama.rs:139-147).
   dequantize(w, scales, biases, group_size, bits)
       mlx_rs::ops::dequantize as used at src/engine/mlx_lm/utils/moe.rs:118-126.
+  gather_qmm(x, w, scales, biases, rhs_indices, transpose, group_size, bits, sorted_indices)
+      the MoE expert matmul wrapped at src/engine/mlx_lm/utils/moe.rs:33-77.
+  QuantizedEmbedding(weight, scales, biases, group_size, bits)
+      lookup (src/engine/mlx_lm/models/bonsai_q1.rs:603-613) and as_linear, the tied
+      lm_head (src/engine/mlx_lm/models/llama.rs:511-517).
 
 Errors are raised as MiqmmError, the counterpart of mlx-rs's Exception built from
 a nonzero mlx-c status (moe.rs:66-76).  Every call goes through libmiqmm.so;
@@ -30,7 +35,7 @@ import torch
 __all__ = [
     "MiqmmError", "quantized_matmul", "quantized_linear", "QuantizedLinear", "dequantize",
     "unpack", "synth_problem", "query_route", "result_type", "lib", "LIB_PATH", "quantized_matmul_grouped",
-    "Problem",
+    "Problem", "gather_qmm", "quantized_embedding", "QuantizedEmbedding",
     "OK", "EINVAL", "ENOTSUP", "EHIP", "ROUTE_AUTO", "ROUTE_QMV", "ROUTE_QMM", "ROUTE_QMV_DOT", "ROUTE_QMVX",
 ]
 
@@ -79,6 +84,7 @@ def lib() -> ctypes.CDLL:
     L.miqmm_synth_problem.argtypes = [P, P, P, P, I64, I64, I64, I, I, I, I, U64, U64, P]
     L.miqmm_quantized_matmul_grouped.argtypes = [ctypes.POINTER(Problem), I, I64, I64, I, I, I, I, I, P]
     L.miqmm_gather_qmm.argtypes = [P, P, P, P, P, P, I64, I64, I, I64, I64, I64, I64, I, I, I, I, I, I, I, P]
+    L.miqmm_quantized_embedding.argtypes = [P, P, I64, P, P, P, I64, I64, I, I, I, I, P]
     for name in ("miqmm_quantized_matmul", "miqmm_quantized_matmul_ex", "miqmm_quantized_linear",
                  "miqmm_dequantize", "miqmm_unpack", "miqmm_query_route", "miqmm_synth_problem",
                  "miqmm_quantized_matmul_grouped"):
@@ -274,6 +280,50 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
                                   top_k, per_index, M, N, K, E, int(bool(transpose)), group_size, bits, _dt(xc),
                                   _dt(scales), _dt(out), int(bool(sorted_indices)), _stream(stream)))
     return out
+
+
+def quantized_embedding(ids: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                        group_size: int = 64, bits: int = 4, *, dtype: Optional[torch.dtype] = None,
+                        out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """out[..., k] = dequantize(w[ids], scales[ids], biases[ids]): the lookup of a
+    quantized embedding table as the reference restates it
+    (src/engine/mlx_lm/models/bonsai_q1.rs:603-613: take rows, then dequantize).
+    The result is ids.shape + (K,) in `dtype` (default: the scales' dtype, as
+    MLX's dequantize returns); an id outside [0, V) gives a zero row."""
+    V, K = _check_weights(w, scales, biases, group_size, bits)
+    if ids.dtype.is_floating_point or ids.dtype == torch.bool:
+        raise MiqmmError(EINVAL, f"ids must hold integers, got {ids.dtype}")
+    idc = ids.to(torch.int32).contiguous()
+    dt = dtype or scales.dtype
+    shape = tuple(ids.shape) + (K,)
+    if out is None:
+        out = torch.empty(shape, dtype=dt, device=w.device)
+    elif out.shape != shape or not out.is_contiguous() or out.dtype != dt:
+        raise MiqmmError(EINVAL, f"out must be contiguous {shape} of {dt}")
+    _check(lib().miqmm_quantized_embedding(_ptr(out), _ptr(idc), idc.numel(), _ptr(w), _ptr(scales), _ptr(biases),
+                                           V, K, group_size, bits, _dt(scales), _dt(out), _stream(stream)))
+    return out
+
+
+class QuantizedEmbedding:
+    """mlx-rs QuantizedEmbedding: `forward(ids)` looks rows up (the step before
+    the first projection of each token), `as_linear(x)` is the tied lm_head,
+    quantized_matmul(x, weight, scales, biases) (src/engine/mlx_lm/models/llama.rs:511-517)."""
+
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 group_size: int = 64, bits: int = 4):
+        self.weight, self.scales, self.biases = weight, scales, biases
+        self.group_size, self.bits = group_size, bits
+        _check_weights(weight, scales, biases, group_size, bits)
+
+    def __call__(self, ids: torch.Tensor, **kw) -> torch.Tensor:
+        return self.forward(ids, **kw)
+
+    def forward(self, ids: torch.Tensor, **kw) -> torch.Tensor:
+        return quantized_embedding(ids, self.weight, self.scales, self.biases, self.group_size, self.bits, **kw)
+
+    def as_linear(self, x: torch.Tensor, **kw) -> torch.Tensor:
+        return quantized_matmul(x, self.weight, self.scales, self.biases, True, self.group_size, self.bits, **kw)
 
 
 def quantized_linear(x, w, scales, biases, bias=None, group_size: int = 64, bits: int = 4, **kw):

@@ -125,6 +125,20 @@ def test_gather_entry_point_validates(lib):
     assert G(M=0, idx=None, y=None) == miqmm.OK
 
 
+def test_embedding_entry_point_validates(lib):
+    import miqmm
+
+    P = ctypes.c_void_p(16)
+    E = lib.miqmm_quantized_embedding
+    assert E(P, P, 4, P, P, P, 100, 96, 64, 4, 0, 0, None) == miqmm.EINVAL  # K % g
+    assert E(P, P, 4, P, P, P, 100, 128, 64, 3, 0, 0, None) == miqmm.ENOTSUP
+    assert E(P, P, 4, P, P, P, 100, 128, 64, 4, 0, 7, None) == miqmm.EINVAL  # out dtype
+    assert E(P, P, -1, P, P, P, 100, 128, 64, 4, 0, 0, None) == miqmm.EINVAL
+    assert E(P, None, 4, P, P, P, 100, 128, 64, 4, 0, 0, None) == miqmm.EINVAL
+    assert E(ctypes.c_void_p(8), P, 4, P, P, P, 100, 128, 64, 4, 0, 0, None) == miqmm.EINVAL  # alignment
+    assert E(None, None, 0, P, P, P, 100, 128, 64, 4, 0, 0, None) == miqmm.OK  # no ids: nothing to do
+
+
 def test_gather_python_shape_checks(lib):
     import torch
 

@@ -348,3 +348,41 @@ def test_gather_pins_reject_planted_mistakes():
     bad_x = O.gather_qmm_f64(x[::-1].copy()[:, None], w, s, b, idx, K, g, bits)
     assert not np.allclose(bad_x, want, atol=1e-3)
     np.testing.assert_allclose(O.gather_qmm_f64(x[:, None], w, s, b, idx, K, g, bits), want, rtol=1e-12)
+
+
+# ------------------------------------------------------------------ embedding lookup
+def test_embedding_known_answer():
+    # one row of 64 4-bit codes 0..15 repeated, group 32: scales (0.5, 2), biases (-1, 3)
+    K, g, bits = 64, 32, 4
+    q = (np.arange(K) % 16).astype(np.uint8).reshape(1, K)
+    w = O.pack(q, bits)
+    s = O.f32_to_bf16(np.array([[0.5, 2.0]], np.float32))
+    b = O.f32_to_bf16(np.array([[-1.0, 3.0]], np.float32))
+    got = O.embedding(np.array([0]), w, s, b, K, g, bits, out_dtype=O.F32)
+    want = np.concatenate([0.5 * (np.arange(32) % 16) - 1.0, 2.0 * (np.arange(32, 64) % 16) + 3.0])
+    np.testing.assert_array_equal(got[0], want.astype(np.float32))
+
+
+def test_embedding_rows_dot_x_equal_quantized_matmul():
+    # the looked-up rows are the rows of dequant(W): dotting them with x gives
+    # quantized_matmul(x, W[ids]) (fp32 dequant vs exact: within 2^-20 relative)
+    V, K, g, bits = 50, 256, 64, 4
+    x, w, s, b = O.synth_problem(1, V, K, g, bits, seed=21)
+    ids = np.array([3, 49, 0, 3, 17])
+    rows = O.embedding(ids, w, s, b, K, g, bits, out_dtype=O.F32).astype(np.float64)
+    xf = O.bf16_to_f32(x).astype(np.float64)[0]
+    want = O.qmm_f64(x, w[ids], s[ids], b[ids], K, g, bits)[0]
+    np.testing.assert_allclose(rows @ xf, want, rtol=1e-5, atol=1e-6)
+    # a planted off-by-one row fails it
+    bad = O.embedding(ids + 1, w, s, b, K, g, bits, out_dtype=O.F32).astype(np.float64)
+    assert not np.allclose(bad @ xf, want, rtol=1e-3, atol=1e-4)
+
+
+def test_embedding_out_of_range_and_rounding():
+    V, K, g, bits = 7, 128, 32, 8
+    _, w, s, b = O.synth_problem(1, V, K, g, bits, seed=22)
+    ids = np.array([[6, -1], [7, 2]])
+    f32 = O.embedding(ids, w, s, b, K, g, bits, out_dtype=O.F32)
+    assert f32.shape == (2, 2, K) and not f32[0, 1].any() and not f32[1, 0].any()
+    h = O.embedding(ids, w, s, b, K, g, bits, out_dtype=O.BF16)
+    np.testing.assert_array_equal(h, O.f32_to_bf16(f32))
