@@ -9,11 +9,12 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "miqmm.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
 
 
 def _declared():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"\b(miqmm_[a-z_]+)\s*\(", text)))
 
 
@@ -27,7 +28,7 @@ def lib():
 def test_exports_every_declared_symbol(lib):
     names = _declared()
     assert {"miqmm_quantized_matmul", "miqmm_quantized_linear", "miqmm_dequantize",
-            "miqmm_unpack", "miqmm_last_error"} <= set(names)
+            "miqmm_unpack", "miqmm_last_error", "miqmm_checkpoint_open"} <= set(names)
     for n in names:
         assert hasattr(lib, n), f"{n} declared in miqmm.h but not exported"
 
