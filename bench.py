@@ -219,6 +219,59 @@ def cpu_baseline(miqmm, torch, projs, budget_s=15.0):
             "ms_per_step": round(el / steps * 1e3, 3)}
 
 
+def graph_avg(torch, fns, launches, reps):
+    """average time of one call, over a HIP graph of `launches` calls cycling
+    through `fns` (one per weight replica, so the weights come cold from HBM)"""
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(launches):
+            fns[i % len(fns)]()
+    g.replay()
+    torch.cuda.synchronize()
+    t = time_graphs(torch, [g], reps)
+    return t / (reps * launches)
+
+
+def moe_and_embedding(miqmm, torch):
+    """the rows after the quantized projections: gather_qmm on DeepSeek-V2-Lite's
+    routed experts (64 experts, top-6, hidden 2048, expert inter 1408, 4-bit g64)
+    and the quantized embedding lookup of Qwen2.5-0.5B (151936 x 896)"""
+    E, H, I, top_k, g = 64, 2048, 1408, 6, 64
+    res = {}
+    stacks = []
+    for r in range(4):  # 4 layers' experts: 4 x 3 x 92 MB, cold in the 256 MB cache
+        gate = [t.reshape(E, I, -1) for t in miqmm.synth_problem(1, E * I, H, g, 4, seed=60 + r, stream_id=1)[1:]]
+        down = [t.reshape(E, H, -1) for t in miqmm.synth_problem(1, E * H, I, g, 4, seed=70 + r, stream_id=2)[1:]]
+        stacks.append((gate, down))
+    for T in (1, 64):
+        gen = torch.Generator().manual_seed(T)
+        idx = torch.stack([torch.randperm(E, generator=gen)[:top_k] for _ in range(T)]).to(torch.int32).cuda()
+        x = torch.randn(T, 1, 1, H, device="cuda").to(torch.bfloat16)
+        h = torch.randn(T, top_k, 1, I, device="cuda").to(torch.bfloat16)
+        yg = torch.empty(T, top_k, 1, I, device="cuda", dtype=torch.bfloat16)
+        yd = torch.empty(T, top_k, 1, H, device="cuda", dtype=torch.bfloat16)
+        tg = graph_avg(torch, [lambda s=s: miqmm.gather_qmm(x, *s[0], idx, True, g, 4, out=yg) for s in stacks],
+                       64, 5)
+        td = graph_avg(torch, [lambda s=s: miqmm.gather_qmm(h, *s[1], idx, True, g, 4, out=yd) for s in stacks],
+                       64, 5)
+        sel = T * top_k * qbytes(1, I, H)  # bytes of the selected experts (each selection streams its expert)
+        res[f"gather_qmm_T{T}"] = {"gate_2048to1408_us": round(tg * 1e6, 2), "down_1408to2048_us": round(td * 1e6, 2),
+                                   "selected_expert_bytes": sel, "gate_GB/s": round(sel / tg / 1e9, 1)}
+    del stacks
+    V, K = 151936, 896
+    tabs = [miqmm.synth_problem(1, V, K, g, 4, seed=80 + r, stream_id=3)[1:] for r in range(3)]
+    for T in (1, 2048):
+        ids = torch.randint(0, V, (T,), device="cuda", dtype=torch.int32)
+        out = torch.empty(T, K, device="cuda", dtype=torch.bfloat16)
+        t = graph_avg(torch, [lambda tb=tb: miqmm.quantized_embedding(ids, *tb, g, 4, out=out) for tb in tabs], 64, 5)
+        nb = T * (K // 2 + 2 * (K // g) * 2 + K * 2)
+        res[f"embedding_T{T}"] = {"us": round(t * 1e6, 2), "bytes": nb, "GB/s": round(nb / t / 1e9, 1)}
+    return res
+
+
 PROFILE_DIR = os.path.join(ROOT, "profiles")
 ROOFLINE_PROFILE = os.path.join(PROFILE_DIR, "qmv_lm_head_151936x896_m1.md")
 
@@ -345,6 +398,10 @@ def main():
         head["qmv_m1_4096x14336"] = {"us": round(avg * 1e6, 3), "GB/s": round(nb / avg / 1e9, 1),
                                      "frac_hbm": round(nb / avg / 1e9 / HBM_PEAK_GBS, 4), "bytes": nb}
         print(f"# qmv 4096x14336 M=1: {avg * 1e6:.2f} us {nb / avg / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+        avg, nb = kernel_roofline(miqmm, torch, 4096, 14336, 1, replicas=24, launches_per_graph=96, reps=6)
+        head["qmv_m1_14336x4096"] = {"us": round(avg * 1e6, 3), "GB/s": round(nb / avg / 1e9, 1),
+                                     "frac_hbm": round(nb / avg / 1e9 / HBM_PEAK_GBS, 4), "bytes": nb}
+        print(f"# qmv 14336x4096 M=1: {avg * 1e6:.2f} us {nb / avg / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
         for (N, K) in [(14336, 4096), (4096, 14336), (6144, 4096), (4096, 4096)]:
             tf, tsec = qmm_tflops(miqmm, torch, 2048, N, K, iters=10)
             head[f"qmm_m2048_{K}to{N}"] = {"TFLOP/s": round(tf, 1), "us": round(tsec * 1e6, 1),
@@ -353,6 +410,9 @@ def main():
         head["dense_bf16_gemm_m2048_4096to14336_torch"] = {
             "TFLOP/s": round(dense_bf16_tflops(torch, 2048, 14336, 4096, 10), 1)}
         out["headline"] = head
+        torch.cuda.empty_cache()
+        out["moe_and_embedding"] = moe_and_embedding(miqmm, torch)
+        print(f"# moe/embedding: {json.dumps(out['moe_and_embedding'])}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
