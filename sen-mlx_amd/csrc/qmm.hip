@@ -40,6 +40,10 @@ namespace miqmm {
 namespace {
 
 constexpr int kBM = 256;
+#ifndef QMM_WDIST
+#define QMM_WDIST 3
+#endif
+constexpr int kWDist = QMM_WDIST;  // k-steps the codes are loaded ahead of their MFMAs
 constexpr int kBK = 64;
 constexpr int kRowBytes = kBK * 2;  // one LDS row: 64 bf16
 
@@ -234,7 +238,7 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     // of t+2, which are LDS writes in flight.
     constexpr int E_PER_KK = (W_CHUNKS + 3) / 4;
     auto step = [&](int t, const WR& cur, WR& nxt) {
-        load_w(t + 2, nxt);
+        load_w(t + kWDist, nxt);
         issue_a(t + 2);
         bf16x8_t af[2][TM], bf[2][TN];
         read_frags(t, 0, af[0], bf[0]);
@@ -259,6 +263,8 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
         MIQMM_WAIT_BARRIER(waitcnt_vm_lgkm0(LOADS));
     };
 
+    int t = 0;
+#if QMM_WDIST == 2
     WR w0, w1;
     // same issue order as the loop, unconditionally (past K the offsets are
     // out of range), so the loop starts with the wait counts it keeps
@@ -268,12 +274,31 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     issue_a(1);
     store_w(0, w0);
     MIQMM_WAIT_BARRIER(waitcnt_vm_lgkm0(LOADS));  // x of step 0 landed
-    int t = 0;
     for (; t + 1 < KT; t += 2) {
         step(t, w1, w0);
         step(t + 1, w0, w1);
     }
     if (t < KT) step(t, w1, w0);
+#else
+    WR w0, w1, w2;
+    // codes run three steps ahead of the MFMAs (x two): at the end of step t
+    // the wait leaves the codes of t+3 and the x of t+2 in flight, so the
+    // codes of t+2, dequantized during step t+1, have landed before it starts
+    load_w(0, w0);
+    issue_a(0);
+    load_w(1, w1);
+    load_w(2, w2);
+    issue_a(1);
+    store_w(0, w0);
+    MIQMM_WAIT_BARRIER(waitcnt_vm_lgkm0(LOADS));  // x of step 0 and codes of step 1 landed
+    for (; t + 2 < KT; t += 3) {
+        step(t, w1, w0);
+        step(t + 1, w2, w1);
+        step(t + 2, w0, w2);
+    }
+    if (t < KT) step(t, w1, w0);
+    if (t + 1 < KT) step(t + 1, w2, w1);
+#endif
     // the prefetches past the last step (out of range, zero-filled) still
     // write the x ring; they must land before the ring is reused below
     MIQMM_WAIT_BARRIER(0x0070);  // vmcnt(0) lgkmcnt(0)
