@@ -157,6 +157,24 @@ int miqmm_dequantize(void* out, const uint32_t* w, const void* scales, const voi
                      void* stream);
 
 /*
+ * miqmm_gather_qmm with a caller-provided device workspace (16-byte aligned,
+ * at least miqmm_gather_qmm_workspace_size bytes).  With M == 1 and enough
+ * selections per expert (prefill-sized batches), the selections are grouped
+ * by expert on the device and each expert's weights are streamed once through
+ * the tiled MFMA matmul (the qmm route's arithmetic: W rounded to bf16 after
+ * the fp32 dequant) instead of once per selection; otherwise, or without a
+ * workspace, this is miqmm_gather_qmm.  No counterpart in the reference (its
+ * wrapper, src/engine/mlx_lm/utils/moe.rs:33-77, always passes
+ * sorted_indices=false): the caller that can pass scratch memory for it.
+ */
+int miqmm_gather_qmm_workspace_size(int64_t batch, int64_t top_k, int64_t experts, int64_t* bytes);
+int miqmm_gather_qmm_ws(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                        const int32_t* rhs_indices, int64_t batch, int64_t top_k, int x_per_index, int64_t M,
+                        int64_t N, int64_t K, int64_t experts, int transpose, int group_size, int bits, int x_dtype,
+                        int sb_dtype, int y_dtype, int sorted_indices, void* workspace, int64_t workspace_bytes,
+                        void* stream);
+
+/*
  * Quantized embedding lookup: out[t, k] = scales[id,k/g] * q[id,k] +
  * biases[id,k/g] (fp32 fma, stored as out_dtype) with id = ids[t], for
  * t < T, from a table of V rows of K codes (w [V, K*bits/32], scales and

@@ -35,6 +35,12 @@ int ok() {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 constexpr int64_t kMaxDim = (int64_t)1 << 31;
+// selections per expert (on average) from which gather_qmm groups them by
+// expert into the tiled matmul, when given a workspace
+#ifndef MIQMM_GROUPED_MIN
+#define MIQMM_GROUPED_MIN 8
+#endif
+constexpr int64_t kGroupedMinPerExpert = MIQMM_GROUPED_MIN;
 
 int check_quant(int64_t N, int64_t K, int group_size, int bits, int sb_dtype) {
     if (bits != 4 && bits != 8) {
@@ -136,6 +142,53 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
     return check_launch(miqmm::launch_qmm(a), "qmm launch");
 }
 
+// gather_qmm: validation, then the expert-grouped tiled matmul when a
+// workspace is given and there are enough selections per expert to fill its
+// M tiles, else the per-selection v_dot2 GEMV
+int gather_common(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                  const int32_t* rhs_indices, int64_t batch, int64_t top_k, int x_per_index, int64_t M, int64_t N,
+                  int64_t K, int64_t experts, int transpose, int group_size, int bits, int x_dtype, int sb_dtype,
+                  int y_dtype, int sorted_indices, void* workspace, int64_t workspace_bytes, void* stream) {
+    (void)sorted_indices;  // a scheduling hint only: every order gives the same result here
+    if (batch < 0 || top_k < 0 || batch >= kMaxDim || top_k >= kMaxDim)
+        return fail(MIQMM_EINVAL, "batch and top_k must be in [0, 2^31), got %lld and %lld", (long long)batch,
+                    (long long)top_k);
+    if (experts <= 0 || experts >= kMaxDim)
+        return fail(MIQMM_EINVAL, "experts must be in [1, 2^31), got %lld", (long long)experts);
+    if (x_per_index != 0 && x_per_index != 1) return fail(MIQMM_EINVAL, "x_per_index must be 0 or 1");
+    if (workspace_bytes < 0) return fail(MIQMM_EINVAL, "workspace_bytes must be >= 0");
+    const int64_t problems = batch * top_k;
+    bool noop;  // no selections or no rows: nothing to read, pointers may be null
+    int st = check_args(y, x, w, scales, biases, problems == 0 ? 0 : M, N, K, transpose, group_size, bits, x_dtype,
+                        sb_dtype, y_dtype, MIQMM_ROUTE_AUTO, &noop);
+    if (st != MIQMM_OK || noop) return st;
+    if (!rhs_indices) return fail(MIQMM_EINVAL, "null pointer argument");
+    if (problems * M * (K > N ? K : N) >= ((int64_t)1 << 40)) return fail(MIQMM_EINVAL, "batch*top_k*M*K too large");
+    const int64_t x_bytes = (x_per_index ? problems : batch) * M * K * 2;
+    if (workspace && M == 1 && problems >= kGroupedMinPerExpert * experts && experts <= 1024 &&
+        x_bytes < ((int64_t)1 << 31) && workspace_bytes >= miqmm::gather_grouped_workspace(problems, experts)) {
+        if (!aligned16(workspace)) return fail(MIQMM_EINVAL, "workspace must be 16-byte aligned");
+        miqmm::QmmArgs a{y, x, w, scales, biases, nullptr, problems, N, K, group_size, bits, x_dtype, sb_dtype,
+                         y_dtype, reinterpret_cast<hipStream_t>(stream)};
+        return check_launch(miqmm::launch_gather_grouped(a, rhs_indices, batch, (int)top_k, x_per_index, experts,
+                                                          x_bytes, workspace),
+                            "grouped gather launch");
+    }
+    // the GEMV handles 16 rows of x per pass over a weight tile; more rows
+    // (rare in decode) take several passes, one per 16-row slice of every matrix
+    const int ysz = y_dtype == MIQMM_DT_F32 ? 4 : 2;
+    for (int64_t m0 = 0; m0 < M; m0 += 16) {
+        miqmm::QmmArgs a{static_cast<char*>(y) + m0 * N * ysz, static_cast<const uint16_t*>(x) + m0 * K, w, scales,
+                         biases, nullptr, M - m0 < 16 ? M - m0 : 16, N, K, group_size, bits, x_dtype, sb_dtype,
+                         y_dtype, reinterpret_cast<hipStream_t>(stream)};
+        st = check_launch(
+            miqmm::launch_qmv_gather(a, rhs_indices, batch, (int)top_k, x_per_index, experts, M * K, M * N),
+            "gather qmv launch");
+        if (st != MIQMM_OK) return st;
+    }
+    return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -220,33 +273,26 @@ int miqmm_gather_qmm(void* y, const void* x, const uint32_t* w, const void* scal
                      const int32_t* rhs_indices, int64_t batch, int64_t top_k, int x_per_index, int64_t M,
                      int64_t N, int64_t K, int64_t experts, int transpose, int group_size, int bits, int x_dtype,
                      int sb_dtype, int y_dtype, int sorted_indices, void* stream) {
-    (void)sorted_indices;  // a scheduling hint only: every order gives the same result here
-    if (batch < 0 || top_k < 0 || batch >= kMaxDim || top_k >= kMaxDim)
-        return fail(MIQMM_EINVAL, "batch and top_k must be in [0, 2^31), got %lld and %lld", (long long)batch,
-                    (long long)top_k);
-    if (experts <= 0 || experts >= kMaxDim)
-        return fail(MIQMM_EINVAL, "experts must be in [1, 2^31), got %lld", (long long)experts);
-    if (x_per_index != 0 && x_per_index != 1) return fail(MIQMM_EINVAL, "x_per_index must be 0 or 1");
-    const int64_t problems = batch * top_k;
-    bool noop;  // no selections or no rows: nothing to read, pointers may be null
-    int st = check_args(y, x, w, scales, biases, problems == 0 ? 0 : M, N, K, transpose, group_size, bits, x_dtype,
-                        sb_dtype, y_dtype, MIQMM_ROUTE_AUTO, &noop);
-    if (st != MIQMM_OK || noop) return st;
-    if (!rhs_indices) return fail(MIQMM_EINVAL, "null pointer argument");
-    if (problems * M * (K > N ? K : N) >= ((int64_t)1 << 40)) return fail(MIQMM_EINVAL, "batch*top_k*M*K too large");
-    // the GEMV handles 16 rows of x per pass over a weight tile; more rows
-    // (rare in decode) take several passes, one per 16-row slice of every matrix
-    const int ysz = y_dtype == MIQMM_DT_F32 ? 4 : 2;
-    for (int64_t m0 = 0; m0 < M; m0 += 16) {
-        miqmm::QmmArgs a{static_cast<char*>(y) + m0 * N * ysz, static_cast<const uint16_t*>(x) + m0 * K, w, scales,
-                         biases, nullptr, M - m0 < 16 ? M - m0 : 16, N, K, group_size, bits, x_dtype, sb_dtype,
-                         y_dtype, reinterpret_cast<hipStream_t>(stream)};
-        st = check_launch(
-            miqmm::launch_qmv_gather(a, rhs_indices, batch, (int)top_k, x_per_index, experts, M * K, M * N),
-            "gather qmv launch");
-        if (st != MIQMM_OK) return st;
-    }
+    return gather_common(y, x, w, scales, biases, rhs_indices, batch, top_k, x_per_index, M, N, K, experts, transpose,
+                         group_size, bits, x_dtype, sb_dtype, y_dtype, sorted_indices, nullptr, 0, stream);
+}
+
+int miqmm_gather_qmm_workspace_size(int64_t batch, int64_t top_k, int64_t experts, int64_t* bytes) {
+    if (!bytes) return fail(MIQMM_EINVAL, "null pointer argument");
+    if (batch < 0 || top_k < 0 || experts <= 0 || batch >= kMaxDim || top_k >= kMaxDim || experts >= kMaxDim)
+        return fail(MIQMM_EINVAL, "batch, top_k and experts out of range");
+    *bytes = miqmm::gather_grouped_workspace(batch * top_k, experts);
     return ok();
+}
+
+int miqmm_gather_qmm_ws(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                        const int32_t* rhs_indices, int64_t batch, int64_t top_k, int x_per_index, int64_t M,
+                        int64_t N, int64_t K, int64_t experts, int transpose, int group_size, int bits, int x_dtype,
+                        int sb_dtype, int y_dtype, int sorted_indices, void* workspace, int64_t workspace_bytes,
+                        void* stream) {
+    return gather_common(y, x, w, scales, biases, rhs_indices, batch, top_k, x_per_index, M, N, K, experts, transpose,
+                         group_size, bits, x_dtype, sb_dtype, y_dtype, sorted_indices, workspace, workspace_bytes,
+                         stream);
 }
 
 int miqmm_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,

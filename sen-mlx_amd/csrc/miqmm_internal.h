@@ -61,6 +61,13 @@ hipError_t launch_qmv_gather(const QmmArgs& a, const int32_t* idx, int64_t T, in
                              int64_t experts, int64_t x_stride, int64_t y_stride);
 hipError_t launch_qmv_mfma(const QmmArgs& a);  // group-diagonal MFMA GEMV
 hipError_t launch_qmm(const QmmArgs& a);
+// expert-grouped gather_qmm on the tiled MFMA matmul (M = 1 per selection):
+// a describes expert 0 (w / scales / biases bases, N, K); T * top_k
+// selections; the workspace holds the grouping (gather_grouped_workspace bytes)
+int64_t gather_grouped_max_tiles(int64_t S, int64_t E);
+int64_t gather_grouped_workspace(int64_t S, int64_t E);
+hipError_t launch_gather_grouped(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_index,
+                                 int64_t experts, int64_t x_bytes, void* workspace);
 hipError_t launch_qmvx(const QmmArgs& a);      // MFMA GEMV, M <= 4, x in LDS
 bool qmvx_supported(int64_t M, int64_t K, int group_size);
 

@@ -103,13 +103,31 @@ struct WRegs {
     uint16_t s[W_PER], b[W_PER];
 };
 
-template <int BITS, int SBT, int BN>
+// The expert-grouped matmul (GATHER): each M tile holds up to 256 selections
+// of one expert, listed by gather_plan_kernel; its x rows are gathered through
+// the selection list and its output rows scattered back, and W, scales and
+// biases are the expert's slices of the stacked tensors.
+struct QmmGather {
+    const int32_t* perm;    // selection ids grouped by expert
+    const int32_t* seg;     // seg[e] .. seg[e+1]: expert e's range of perm (e == E: invalid ids)
+    const int32_t* tiles;   // (expert, first position in perm) of each M tile
+    const int32_t* ntiles;  // number of M tiles
+    int top_k, x_per_index, experts;
+    uint32_t x_bytes;       // bytes of x (all its matrices)
+};
+
+__device__ __forceinline__ int sload(const int32_t* p) {
+    return __builtin_amdgcn_readfirstlane(*(const __attribute__((address_space(4))) int32_t*)p);
+}
+
+template <int BITS, int SBT, int BN, bool GATHER>
 __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict__ x,
                                                      const uint32_t* __restrict__ w,
                                                      const uint16_t* __restrict__ sc,
                                                      const uint16_t* __restrict__ bi,
                                                      void* __restrict__ y, const void* __restrict__ bias,
-                                                     int M, int N, int K, int gs_shift, int y_dtype) {
+                                                     int M, int N, int K, int gs_shift, int y_dtype,
+                                                     const QmmGather gq) {
     constexpr int WN = BN / 2;                    // wave tile 128 x WN
     constexpr int TM = 4, TN = WN / 32;           // 32x32 MFMA tiles per wave
     constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk
@@ -134,11 +152,32 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     const uint32_t xrow = (uint32_t)K * 2;
     const uint32_t wrow = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
-    const int mrows = min(kBM, M - m0), nrows = min(BN, N - n0);
-    const auto xr = make_rsrc(x + (size_t)m0 * K, (uint32_t)mrows * xrow);
-    const auto wr = make_rsrc((const char*)w + (size_t)n0 * wrow, (uint32_t)nrows * wrow);
-    const auto sr = make_rsrc(sc + (size_t)n0 * G, (uint32_t)nrows * G * 2);
-    const auto br = make_rsrc(bi + (size_t)n0 * G, (uint32_t)nrows * G * 2);
+    int mrows = min(kBM, M - m0), nrows = min(BN, N - n0);
+    int p0 = 0;           // GATHER: first position of this tile in the selection list
+    size_t erow0 = 0;     // GATHER: first W row of the expert
+    if constexpr (GATHER) {
+        if ((int)blockIdx.y >= sload(gq.ntiles)) return;  // block-uniform: past the listed tiles
+        const int e = sload(gq.tiles + 2 * blockIdx.y);
+        p0 = sload(gq.tiles + 2 * blockIdx.y + 1);
+        mrows = min(kBM, sload(gq.seg + e + 1) - p0);
+        if (e >= gq.experts) nrows = 0;  // out-of-range ids: zero rows
+        erow0 = (size_t)min(e, gq.experts - 1) * N;
+    }
+    const auto xr = GATHER ? make_rsrc(x, gq.x_bytes) : make_rsrc(x + (size_t)m0 * K, (uint32_t)mrows * xrow);
+    const auto wr = make_rsrc((const char*)w + (erow0 + n0) * wrow, (uint32_t)nrows * wrow);
+    const auto sr = make_rsrc(sc + (erow0 + n0) * G, (uint32_t)nrows * G * 2);
+    const auto br = make_rsrc(bi + (erow0 + n0) * G, (uint32_t)nrows * G * 2);
+    // GATHER: byte offset of the x row of each of this lane's eight copy rows
+    uint32_t xbase[8];
+    if constexpr (GATHER) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int row = j * 32 + (lane >> 1);
+            const int sel = row < mrows ? gq.perm[p0 + row] : -1;
+            const int xi = gq.x_per_index ? sel : sel / gq.top_k;
+            xbase[j] = sel >= 0 ? (uint32_t)xi * xrow : kOOB;
+        }
+    }
 
     // x tile -> LDS: wave `wid` fills k-slice `wid` ([256 rows x 32 B]) with
     // eight 1 KiB instructions; lane i of an instruction lands at byte 16*i,
@@ -152,7 +191,9 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
             const int row = j * 32 + (lane >> 1);
             const int fk = (lane & 1) ^ ((row >> 3) & 1);
             const int k = kb + fk * 8;
-            const uint32_t off = k < K ? (uint32_t)row * xrow + (uint32_t)k * 2 : kOOB;
+            uint32_t off;
+            if constexpr (GATHER) off = k < K ? xbase[j] + (uint32_t)k * 2 : kOOB;
+            else off = k < K ? (uint32_t)row * xrow + (uint32_t)k * 2 : kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(slice + j * 1024), 16, off, 0, 0, 0);
         }
     };
@@ -326,8 +367,15 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
 #pragma unroll 1
         for (int p = lane; p < 32 * RUNS; p += 64) {
             const int row = p / RUNS, c8 = p % RUNS;
-            const int gr = wrow0 + i * 32 + row, gc = wcol0 + c8 * 8;
-            if (gr >= M || gc >= N) continue;
+            int gr = wrow0 + i * 32 + row;
+            const int gc = wcol0 + c8 * 8;
+            if constexpr (GATHER) {  // the tile's row -> its selection, one output row each
+                const int lr = gr - m0;
+                if (lr >= mrows || gc >= N) continue;
+                gr = gq.perm[p0 + lr];
+            } else {
+                if (gr >= M || gc >= N) continue;
+            }
             const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(stage + row * ES + c8 * 8);
             const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(stage + row * ES + c8 * 8 + 4);
             const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
@@ -360,22 +408,61 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     }
 }
 
-template <int BITS, int SBT, int BN>
-hipError_t launch_t(const QmmArgs& a) {
+template <int BITS, int SBT, int BN, bool GATHER>
+hipError_t launch_t(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles) {
     constexpr size_t lds = 3 * (size_t)kBM * kRowBytes + 2 * (size_t)BN * kRowBytes;
     static bool attr_set = false;  // the attribute is per kernel; setting it twice is harmless
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)qmm_kernel<BITS, SBT, BN>,
+        hipError_t e = hipFuncSetAttribute((const void*)qmm_kernel<BITS, SBT, BN, GATHER>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    const dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + kBM - 1) / kBM));
+    const dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)m_tiles);
     const int gs_shift = __builtin_ctz((unsigned)a.group_size);
-    hipLaunchKernelGGL((qmm_kernel<BITS, SBT, BN>), grid, dim3(256), lds, a.stream, (const uint16_t*)a.x, a.w,
-                       (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y, a.bias, (int)a.M, (int)a.N,
-                       (int)a.K, gs_shift, a.y_dtype);
+    hipLaunchKernelGGL((qmm_kernel<BITS, SBT, BN, GATHER>), grid, dim3(256), lds, a.stream, (const uint16_t*)a.x,
+                       a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y, a.bias, (int)a.M, (int)a.N,
+                       (int)a.K, gs_shift, a.y_dtype, gq);
     return hipGetLastError();
+}
+
+// One block groups the selections by expert for the expert-grouped matmul:
+// a histogram of the indices in LDS, its prefix sum (the experts' ranges of
+// the selection list; ids outside [0, E) form range E), the selections
+// placed into their ranges, and the list of 256-row M tiles.  The order of
+// selections inside a range is arbitrary; every output row is computed on its
+// own, so the results do not depend on it.
+__global__ __launch_bounds__(1024) void gather_plan_kernel(const int32_t* idx, int S, int E, int32_t* seg,
+                                                           int32_t* ntiles, int32_t* perm, int32_t* tiles) {
+    extern __shared__ int32_t cnt[];  // [E + 1] counts, then [E + 1] fill positions
+    int32_t* pos = cnt + E + 1;
+    for (int e = threadIdx.x; e <= E; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < S; i += blockDim.x) {
+        const int e = idx[i];
+        atomicAdd(&cnt[e >= 0 && e < E ? e : E], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0, t = 0;
+        for (int e = 0; e <= E; ++e) {
+            seg[e] = run;
+            pos[e] = run;
+            for (int r = 0; r < cnt[e]; r += kBM) {
+                tiles[2 * t] = e;
+                tiles[2 * t + 1] = run + r;
+                ++t;
+            }
+            run += cnt[e];
+        }
+        seg[E + 1] = run;
+        *ntiles = t;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < S; i += blockDim.x) {
+        const int e = idx[i];
+        perm[atomicAdd(&pos[e >= 0 && e < E ? e : E], 1)] = i;
+    }
 }
 
 // 256-wide tiles unless that leaves fewer tiles than CUs while 128-wide would not
@@ -388,7 +475,18 @@ int pick_bn(int64_t M, int64_t N) {
 
 template <int BITS, int SBT>
 hipError_t launch_bn(const QmmArgs& a) {
-    return pick_bn(a.M, a.N) == 256 ? launch_t<BITS, SBT, 256>(a) : launch_t<BITS, SBT, 128>(a);
+    const QmmGather none{};
+    const int64_t mt = (a.M + kBM - 1) / kBM;
+    return pick_bn(a.M, a.N) == 256 ? launch_t<BITS, SBT, 256, false>(a, none, mt)
+                                    : launch_t<BITS, SBT, 128, false>(a, none, mt);
+}
+
+template <int BITS, int SBT>
+hipError_t launch_gather_bn(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles) {
+    // the expert-grouped grid has as many M tiles as experts or more: 128-wide
+    // tiles fill the chip whenever 256-wide ones would not
+    return pick_bn(kBM * m_tiles, a.N) == 256 ? launch_t<BITS, SBT, 256, true>(a, gq, m_tiles)
+                                               : launch_t<BITS, SBT, 128, true>(a, gq, m_tiles);
 }
 
 }  // namespace
@@ -402,6 +500,32 @@ void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk) {
 hipError_t launch_qmm(const QmmArgs& a) {
     if (a.bits == 4) return a.sb_dtype == DT_F16 ? launch_bn<4, DT_F16>(a) : launch_bn<4, DT_BF16>(a);
     return a.sb_dtype == DT_F16 ? launch_bn<8, DT_F16>(a) : launch_bn<8, DT_BF16>(a);
+}
+
+int64_t gather_grouped_workspace(int64_t S, int64_t E) {
+    return 4 * ((E + 2) + 1 + S + 2 * gather_grouped_max_tiles(S, E));
+}
+
+int64_t gather_grouped_max_tiles(int64_t S, int64_t E) { return S / kBM + E + 1; }
+
+hipError_t launch_gather_grouped(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_index,
+                                 int64_t experts, int64_t x_bytes, void* workspace) {
+    const int64_t S = T * top_k;
+    int32_t* ws = static_cast<int32_t*>(workspace);
+    int32_t* seg = ws;
+    int32_t* ntiles = seg + experts + 2;
+    int32_t* perm = ntiles + 1;
+    int32_t* tiles = perm + S;
+    const int64_t mt = gather_grouped_max_tiles(S, experts);
+    const size_t plan_lds = 2 * (size_t)(experts + 1) * sizeof(int32_t);
+    hipLaunchKernelGGL(gather_plan_kernel, dim3(1), dim3(1024), plan_lds, a.stream, idx, (int)S, (int)experts, seg,
+                       ntiles, perm, tiles);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const QmmGather gq{perm, seg, tiles, ntiles, top_k, x_per_index, (int)experts, (uint32_t)x_bytes};
+    if (a.bits == 4)
+        return a.sb_dtype == DT_F16 ? launch_gather_bn<4, DT_F16>(a, gq, mt) : launch_gather_bn<4, DT_BF16>(a, gq, mt);
+    return a.sb_dtype == DT_F16 ? launch_gather_bn<8, DT_F16>(a, gq, mt) : launch_gather_bn<8, DT_BF16>(a, gq, mt);
 }
 
 }  // namespace miqmm

@@ -85,6 +85,9 @@ def lib() -> ctypes.CDLL:
     L.miqmm_quantized_matmul_grouped.argtypes = [ctypes.POINTER(Problem), I, I64, I64, I, I, I, I, I, P]
     L.miqmm_gather_qmm.argtypes = [P, P, P, P, P, P, I64, I64, I, I64, I64, I64, I64, I, I, I, I, I, I, I, P]
     L.miqmm_quantized_embedding.argtypes = [P, P, I64, P, P, P, I64, I64, I, I, I, I, P]
+    L.miqmm_gather_qmm_workspace_size.argtypes = [I64, I64, I64, ctypes.POINTER(I64)]
+    L.miqmm_gather_qmm_ws.argtypes = [P, P, P, P, P, P, I64, I64, I, I64, I64, I64, I64, I, I, I, I, I, I, I, P,
+                                      I64, P]
     for name in ("miqmm_quantized_matmul", "miqmm_quantized_matmul_ex", "miqmm_quantized_linear",
                  "miqmm_dequantize", "miqmm_unpack", "miqmm_query_route", "miqmm_synth_problem",
                  "miqmm_quantized_matmul_grouped"):
@@ -222,10 +225,13 @@ def quantized_matmul_grouped(xs, ws, scales, biases, group_size: int = 64, bits:
     return outs
 
 
+GROUPED_MIN_PER_EXPERT = 8  # selections per expert from which the grouped path is used (api.cpp)
+
+
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
                rhs_indices: torch.Tensor, transpose: bool = True, group_size: int = 64, bits: int = 4,
                sorted_indices: bool = False, *, out: Optional[torch.Tensor] = None,
-               stream=None) -> torch.Tensor:
+               stream=None, grouped: Optional[bool] = None) -> torch.Tensor:
     """out[b] = x[b] @ dequant(w[rhs_indices[b]]).T over the broadcast batch b.
 
     Argument order and meaning follow the reference's gather_qmm wrapper
@@ -233,7 +239,10 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
     stacked experts [E, N, K*bits/32], scales/biases [E, N, K/group_size],
     x [..., M, K] whose batch dims broadcast against rhs_indices [...];
     the result is [*broadcast, M, N].  An index outside [0, E) gives zero rows.
-    sorted_indices is a hint that changes nothing here."""
+    sorted_indices is a hint that changes nothing here.  With M == 1 and many
+    selections per expert (grouped=None: the library decides; True/False:
+    pass or withhold the workspace) the selections are grouped by expert and
+    each expert's weights are read once (miqmm_gather_qmm_ws)."""
     if w.dim() != 3 or scales.dim() != 3 or biases.shape != scales.shape or scales.shape[0] != w.shape[0]:
         raise MiqmmError(EINVAL, f"w {tuple(w.shape)} and scales/biases {tuple(scales.shape)}/"
                                  f"{tuple(biases.shape)} must be stacked [E, N, ...] with equal shapes")
@@ -276,9 +285,16 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
         out = torch.empty(shape, dtype=ydt, device=x.device)
     elif out.shape != shape or not out.is_contiguous() or out.dtype != ydt:
         raise MiqmmError(EINVAL, f"out must be contiguous {shape} of {ydt}")
-    _check(lib().miqmm_gather_qmm(_ptr(out), _ptr(xc), _ptr(w), _ptr(scales), _ptr(biases), _ptr(idx), batch,
-                                  top_k, per_index, M, N, K, E, int(bool(transpose)), group_size, bits, _dt(xc),
-                                  _dt(scales), _dt(out), int(bool(sorted_indices)), _stream(stream)))
+    ws, ws_bytes = None, 0
+    if grouped is not False and M == 1 and batch * top_k >= GROUPED_MIN_PER_EXPERT * E:
+        nb = ctypes.c_int64()
+        _check(lib().miqmm_gather_qmm_workspace_size(batch, top_k, E, ctypes.byref(nb)))
+        ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=x.device)
+        ws_bytes = nb.value
+    _check(lib().miqmm_gather_qmm_ws(_ptr(out), _ptr(xc), _ptr(w), _ptr(scales), _ptr(biases), _ptr(idx), batch,
+                                     top_k, per_index, M, N, K, E, int(bool(transpose)), group_size, bits, _dt(xc),
+                                     _dt(scales), _dt(out), int(bool(sorted_indices)), _ptr(ws), ws_bytes,
+                                     _stream(stream)))
     return out
 
 

@@ -126,6 +126,21 @@ def test_gather_entry_point_validates(lib):
     assert G(M=0, idx=None, y=None) == miqmm.OK
 
 
+def test_gather_workspace_entry_points_validate(lib):
+    import miqmm
+
+    nb = ctypes.c_int64()
+    assert lib.miqmm_gather_qmm_workspace_size(1024, 6, 64, ctypes.byref(nb)) == miqmm.OK
+    assert nb.value >= 4 * (1024 * 6 + 64)
+    assert lib.miqmm_gather_qmm_workspace_size(1, 6, 0, ctypes.byref(nb)) == miqmm.EINVAL
+    P = ctypes.c_void_p(16)
+    W = lib.miqmm_gather_qmm_ws
+    args = [P, P, P, P, P, P, 1024, 6, 0, 1, 64, 128, 8, 1, 64, 4, 0, 0, 0, 0]
+    assert W(*args, P, -1, None) == miqmm.EINVAL  # negative workspace size
+    assert W(*args[:8], 2, *args[9:], P, 0, None) == miqmm.EINVAL  # x_per_index
+    assert W(*args[:13], 0, *args[14:], P, 0, None) == miqmm.ENOTSUP  # transpose
+
+
 def test_embedding_entry_point_validates(lib):
     import miqmm
 

@@ -182,3 +182,63 @@ def test_gather_broadcast_forms(gpu, c_oracle):
     check(y3, O.gather_qmm_f64(x, w, u16(sh), u16(bh), idx, K, g, bits, sb_dtype=O.F16), True, "fp16 scales")
     y4 = m.gather_qmm(xd, wd, sd, bd, torch.zeros((0, 2), dtype=torch.int32, device="cuda"), True, g, bits)
     assert y4.shape == (0, 2, 2, N)
+
+
+# (bits, g, scale dtype, E, N, K, tokens, top_k, x shared) -- enough selections per expert for the
+# expert-grouped tiled matmul (>= 8 on average)
+GROUPED = [
+    (4, 64, O.BF16, 8, 256, 512, 128, 2, True),
+    (4, 32, O.F16, 4, 200, 256, 64, 2, False),
+    (8, 64, O.BF16, 6, 136, 384, 100, 3, True),
+    (4, 128, O.BF16, 2, 320, 1024, 300, 1, False),
+]
+
+
+@pytest.mark.parametrize("bits,g,sbd,E,N,K,T,top_k,shared", GROUPED)
+def test_gather_grouped_matches_oracle(gpu, c_oracle, bits, g, sbd, E, N, K, T, top_k, shared):
+    """the expert-grouped path (selections grouped by expert on the device,
+    each expert streamed once through the tiled MFMA matmul) against the
+    oracle, with out-of-range ids among them; held to the qmm route's bar"""
+    m = _miqmm()
+    (w, s, b), (wd, sd, bd) = _experts(E, N, K, g, bits, sbd, seed=E * 7 + K)
+    rng = np.random.default_rng(N + T)
+    idx = rng.integers(0, E, size=(T, top_k)).astype(np.int32)
+    idx[rng.integers(0, T, size=3), 0] = E + 5  # out of range: zero rows
+    xshape = (T, 1, 1) if shared else (T, top_k, 1)
+    x, xd = _x(xshape, K, seed=T)
+    y = m.gather_qmm(xd, wd, sd, bd, torch.from_numpy(idx).cuda(), True, g, bits, grouped=True)
+    assert y.shape == (T, top_k, 1, N)
+    ref = O.gather_qmm_f64(x, w, s, b, idx, K, g, bits, sb_dtype=sbd)
+    check(y, ref, False, f"grouped bits={bits} g={g} E={E} N={N} K={K} T={T} k={top_k} shared={shared}")
+    bad = np.argwhere(idx >= E)
+    yf = y.float().cpu().numpy()
+    for t, j in bad:
+        assert not yf[t, j].any()
+
+
+def test_gather_grouped_deepseek_prefill(gpu, c_oracle):
+    """DeepSeek-V2-Lite experts at a 1024-token prefill (6144 selections over
+    64 experts): grouped and per-selection paths agree within the bar, and
+    sampled selections meet the oracle"""
+    m = _miqmm()
+    E, H, I, top_k, g, T = 64, 2048, 1408, 6, 64, 1024
+    gate = m.synth_problem(1, E * I, H, g, 4, seed=1, stream_id=1)[1:]
+    gw, gs, gb = (t.reshape(E, I, -1) for t in gate)
+    gen = torch.Generator().manual_seed(5)
+    idx = torch.stack([torch.randperm(E, generator=gen)[:top_k] for _ in range(T)]).to(torch.int32).cuda()
+    x = m.synth_problem(T, 8, H, g, 4, seed=3, stream_id=9)[0].reshape(T, 1, 1, H)
+    yg = m.gather_qmm(x, gw, gs, gb, idx, True, g, 4, grouped=True)
+    ys = m.gather_qmm(x, gw, gs, gb, idx, True, g, 4, grouped=False)
+    torch.cuda.synchronize()
+    rep = O.parity_report(yg.float().cpu().numpy(), ys.float().cpu().numpy().astype(np.float64))
+    assert rep["max_err"] <= rep["mag_bar"] and rep["max_err"] <= rep["ulp2_bar"], rep
+    idx_h = idx.cpu().numpy()
+    xs = u16(x)
+    for t in (0, 511, 1023):
+        for j in range(top_k):
+            e = int(idx_h[t, j])
+            w_n = gw[e].cpu().contiguous().view(torch.int32).numpy().view(np.uint32)
+            s_n = gs[e].cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+            b_n = gb[e].cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+            ref = O.qmm_f64(xs[t, 0], w_n, s_n, b_n, H, g, 4)
+            check(yg[t, j], ref, False, f"prefill t={t} j={j}")
