@@ -40,10 +40,13 @@ namespace miqmm {
 namespace {
 
 constexpr int kBM = 256;
-#ifndef QMM_WDIST
-#define QMM_WDIST 3
+#ifndef QMM_XST128
+#define QMM_XST128 3
 #endif
-constexpr int kWDist = QMM_WDIST;  // k-steps the codes are loaded ahead of their MFMAs
+// x ring depth (LDS stages of the x tile) per tile width: the x tile of step
+// t is copied XST-1 steps ahead, and the codes XST steps ahead
+template <int BN>
+constexpr int x_stages() { return BN == 128 ? QMM_XST128 : 3; }
 constexpr int kBK = 64;
 constexpr int kRowBytes = kBK * 2;  // one LDS row: 64 bf16
 
@@ -120,33 +123,65 @@ __device__ __forceinline__ int sload(const int32_t* p) {
     return __builtin_amdgcn_readfirstlane(*(const __attribute__((address_space(4))) int32_t*)p);
 }
 
+// Waves per block.  Eight (two per SIMD: one wave's dequant VALU and LDS
+// traffic overlap the other's MFMAs) for 256-wide tiles, whose waves keep
+// 128 x 64 tiles, and for 8-bit codes; four for 4-bit 128-wide tiles, where
+// eight waves would shrink the wave tile to 64 x 64 and raise the LDS reads
+// per MFMA (measured on MI355X, M = 2048: 830 vs 720 TFLOP/s at N = 14336,
+// 750 vs 870 at 14336 -> 4096).
+template <int BITS, int BN>
+constexpr int waves_per_block() { return BN == 256 || BITS == 8 ? 8 : 4; }
+
+// dynamic LDS: the x ring, two W stages, and one 16-byte slot per idle W thread
+template <int BITS, int BN>
+constexpr size_t qmm_lds_bytes() {
+    constexpr int NT = 64 * waves_per_block<BITS, BN>();
+    constexpr int W_CH = BN * (kBK >> (BITS == 4 ? 5 : 4));
+    constexpr int W_PER = W_CH >= NT ? W_CH / NT : 1;
+    constexpr int idle = NT - W_CH / W_PER;
+    return (size_t)x_stages<BN>() * kBM * kRowBytes + 2 * (size_t)BN * kRowBytes + (idle > 0 ? idle : 0) * 16;
+}
+
 template <int BITS, int SBT, int BN, bool GATHER>
-__global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_kernel(const uint16_t* __restrict__ x,
                                                      const uint32_t* __restrict__ w,
                                                      const uint16_t* __restrict__ sc,
                                                      const uint16_t* __restrict__ bi,
                                                      void* __restrict__ y, const void* __restrict__ bias,
                                                      int M, int N, int K, int gs_shift, int y_dtype,
                                                      const QmmGather gq) {
-    constexpr int WN = BN / 2;                    // wave tile 128 x WN
-    constexpr int TM = 4, TN = WN / 32;           // 32x32 MFMA tiles per wave
+    constexpr int NW = waves_per_block<BITS, BN>(), NT = 64 * NW;
+    // wave grid GM x GN: 2 x 2 for four waves; 2 x 4 (BN = 256) or 4 x 2 (BN = 128) for eight
+    constexpr int GN = NW == 4 ? 2 : (BN == 256 ? 4 : 2), GM = NW / GN;
+    constexpr int WM = kBM / GM, WN = BN / GN;    // wave tile WM x WN
+    constexpr int TM = WM / 32, TN = WN / 32;     // 32x32 MFMA tiles per wave
+    constexpr int XI = 32 / NW;                   // 1 KiB x copies per wave per k-step
     constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk
     constexpr int CPR = kBK >> CPC_SHIFT;         // code chunks per W row per k-step (2 or 4)
-    constexpr int W_PER = BN * CPR / 256;         // code chunks per thread (1, 2 or 4)
+    constexpr int W_CH = BN * CPR;                // code chunks per k-step
+    constexpr int W_PER = W_CH >= NT ? W_CH / NT : 1;  // code chunks per thread (1, 2 or 4)
+    // threads past W_CH / W_PER (4-bit, BN = 128, eight waves) load out of
+    // range (zeros) and store into a dummy LDS slot, with no branch
+    constexpr int XST = x_stages<BN>();           // x ring stages
+    constexpr int XD = XST - 1;                   // k-steps the x tile is copied ahead
+    constexpr int WD = XST;                       // k-steps the codes are loaded ahead
     constexpr int A_STAGE = kBM * kRowBytes;      // 32 KiB
     constexpr int B_STAGE = BN * kRowBytes;
-    constexpr int B_BASE = 3 * A_STAGE;
+    constexpr int B_BASE = XST * A_STAGE;
+    constexpr int DUMMY = B_BASE + 2 * B_STAGE;   // LDS slots of the idle threads' W stores
+    static_assert(NW * 32 * (WN + 32) * 4 <= (int)qmm_lds_bytes<BITS, BN>(), "epilogue staging fits");
     static_assert(W_PER >= 1 && CPR % W_PER == 0, "code chunks per thread");
-    // vector-memory loads one thread issues per k-step: 8 x copies + codes,
+    // vector-memory loads one thread issues per k-step: XI x copies + codes,
     // scales and biases of W_PER chunks
-    constexpr int LOADS = 8 + 3 * W_PER;
-    static_assert(LOADS < 64, "vmcnt range");
+    constexpr int LOADS = XI + 3 * W_PER;
+    static_assert((XD - 1) * LOADS < 64, "vmcnt range");
+    static_assert(WD >= XD + 1, "codes of t+2 issued before the x tile of t+1");
 
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wid >> 1, wn = wid & 1;
+    const int wm = wid / GN, wn = wid % GN;
     const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * BN;
     const int KT = (K + kBK - 1) / kBK;
     const uint32_t xrow = (uint32_t)K * 2;
@@ -167,28 +202,30 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     const auto wr = make_rsrc((const char*)w + (erow0 + n0) * wrow, (uint32_t)nrows * wrow);
     const auto sr = make_rsrc(sc + (erow0 + n0) * G, (uint32_t)nrows * G * 2);
     const auto br = make_rsrc(bi + (erow0 + n0) * G, (uint32_t)nrows * G * 2);
-    // GATHER: byte offset of the x row of each of this lane's eight copy rows
-    uint32_t xbase[8];
+    // x copies: wave `wid` fills rows xrow0 .. xrow0 + 32*XI of k-slice wid % 4
+    const int xslice = wid & 3, xrow0 = (wid >> 2) * XI * 32;
+    // GATHER: byte offset of the x row of each of this lane's copy rows
+    uint32_t xbase[XI];
     if constexpr (GATHER) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int row = j * 32 + (lane >> 1);
+        for (int j = 0; j < XI; ++j) {
+            const int row = xrow0 + j * 32 + (lane >> 1);
             const int sel = row < mrows ? gq.perm[p0 + row] : -1;
             const int xi = gq.x_per_index ? sel : sel / gq.top_k;
             xbase[j] = sel >= 0 ? (uint32_t)xi * xrow : kOOB;
         }
     }
 
-    // x tile -> LDS: wave `wid` fills k-slice `wid` ([256 rows x 32 B]) with
-    // eight 1 KiB instructions; lane i of an instruction lands at byte 16*i,
-    // i.e. row i/2 of its 32-row group, stored half i%2, so it loads logical
-    // half (i%2) ^ (bit 3 of the row)
+    // x tile -> LDS: the k-slice [256 rows x 32 B] is filled by 32-row 1 KiB
+    // instructions; lane i of an instruction lands at byte 16*i, i.e. row i/2
+    // of its 32-row group, stored half i%2, so it loads logical half
+    // (i%2) ^ (bit 3 of the row)
     auto issue_a = [&](int kt) {
-        const int kb = kt * kBK + wid * 16;
-        char* slice = smem + (kt % 3) * A_STAGE + wid * kBM * 32;
+        const int kb = kt * kBK + xslice * 16;
+        char* slice = smem + (kt % XST) * A_STAGE + xslice * kBM * 32 + xrow0 * 32;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int row = j * 32 + (lane >> 1);
+        for (int j = 0; j < XI; ++j) {
+            const int row = xrow0 + j * 32 + (lane >> 1);
             const int fk = (lane & 1) ^ ((row >> 3) & 1);
             const int k = kb + fk * 8;
             uint32_t off;
@@ -201,6 +238,8 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     // this thread's W row and first code chunk
     const int wrow_t = tid / (CPR / W_PER);
     const int wch0 = (tid % (CPR / W_PER)) * W_PER;
+    const bool widle = tid >= W_CH / W_PER;
+    const uint32_t wid_oob = widle ? kOOB : 0u;
     using WR = WRegs<BITS, W_PER>;
     auto load_w = [&](int kt, WR& r) {
         const int kb = kt * kBK;
@@ -208,7 +247,7 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
         for (int i = 0; i < W_PER; ++i) {
             const int kc = kb + ((wch0 + i) << CPC_SHIFT);
             // past the end of K (last step when K % 64 == 32): offsets pushed out of range
-            const uint32_t oob = kc < K ? 0u : kOOB;
+            const uint32_t oob = (kc < K ? 0u : kOOB) | wid_oob;
             r.q[i] = bload16(wr, ((uint32_t)wrow_t * wrow + (uint32_t)kc * BITS / 8) | oob);
             const uint32_t so = (((uint32_t)wrow_t * G + (uint32_t)(kc >> gs_shift)) * 2) | oob;
             r.s[i] = bload2(sr, so);
@@ -227,7 +266,10 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
         u32x4_t o;
         if constexpr (BITS == 4) {
             const uint32_t word = r.q[i][j];
-            const uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
+            uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
+            // opaque to known-bits analysis, so each code converts with one
+            // v_cvt_f32_ubyteN instead of a 4-bit extract plus a convert
+            asm("" : "+v"(lo), "+v"(hi));
             o[0] = pack_bf16x2(fmaf(s, ubyte_f32<0>(lo), b), fmaf(s, ubyte_f32<0>(hi), b));
             o[1] = pack_bf16x2(fmaf(s, ubyte_f32<1>(lo), b), fmaf(s, ubyte_f32<1>(hi), b));
             o[2] = pack_bf16x2(fmaf(s, ubyte_f32<2>(lo), b), fmaf(s, ubyte_f32<2>(hi), b));
@@ -239,7 +281,8 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
             o[2] = pack_bf16x2(fmaf(s, ubyte_f32<0>(w1), b), fmaf(s, ubyte_f32<1>(w1), b));
             o[3] = pack_bf16x2(fmaf(s, ubyte_f32<2>(w1), b), fmaf(s, ubyte_f32<3>(w1), b));
         }
-        *reinterpret_cast<u32x4_t*>(sB + lds_off(BN, wrow_t, c >> 1, c & 1)) = o;
+        char* dst = widle ? smem + DUMMY + (tid - W_CH / W_PER) * 16 : sB + lds_off(BN, wrow_t, c >> 1, c & 1);
+        *reinterpret_cast<u32x4_t*>(dst) = o;
     };
     auto store_w = [&](int kt, const WR& r) {
 #pragma unroll
@@ -259,28 +302,34 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     // per-lane part of a fragment address: row frow of a 32-row tile, half fk
     const uint32_t fbase = (uint32_t)frow * 32 + ((fk ^ ((frow >> 3) & 1)) << 4);
     auto read_frags = [&](int kt, int kk, bf16x8_t* af, bf16x8_t* bf) {
-        const char* sA = smem + (kt % 3) * A_STAGE + fbase;
+        const char* sA = smem + (kt % XST) * A_STAGE + fbase;
         const char* sB = smem + B_BASE + (kt & 1) * B_STAGE + fbase;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
-            af[i] = *reinterpret_cast<const bf16x8_t*>(sA + kk * kBM * 32 + (wm * 128 + i * 32) * 32);
+            af[i] = *reinterpret_cast<const bf16x8_t*>(sA + kk * kBM * 32 + (wm * WM + i * 32) * 32);
 #pragma unroll
         for (int j = 0; j < TN; ++j)
             bf[j] = *reinterpret_cast<const bf16x8_t*>(sB + kk * BN * 32 + (wn * WN + j * 32) * 32);
     };
 
-    // step t: codes of t+2 into `nxt`, x of t+2 into the ring, MFMAs of t,
+    // step t: codes of t+WD into `nxt`, x of t+XD into the ring, MFMAs of t,
     // dequant of t+1 (held in `cur`) spread over the four 16-wide sub-steps so
     // its VALU work issues between MFMAs.  The loads are issued on every step,
     // also past the last one (out-of-range offsets read zeros into a stage
     // nobody reads again): the compiler's wait counts for `cur` are then the
     // same on every path.  The end-of-step barrier is a bare s_barrier with
     // explicit waits, because __syncthreads() would also wait for the x copies
-    // of t+2, which are LDS writes in flight.
+    // still in flight, which are LDS writes.
     constexpr int E_PER_KK = (W_CHUNKS + 3) / 4;
+#ifdef QMM_VPM
+    constexpr int kValuPerMfma = QMM_VPM;
+#else
+    // about 24 VALU per dequantized 16-byte chunk, spread over the sub-step's MFMAs
+    constexpr int kValuPerMfma = (E_PER_KK * 24 + TM * TN - 1) / (TM * TN);
+#endif
     auto step = [&](int t, const WR& cur, WR& nxt) {
-        load_w(t + kWDist, nxt);
-        issue_a(t + 2);
+        load_w(t + WD, nxt);
+        issue_a(t + XD);
         bf16x8_t af[2][TM], bf[2][TN];
         read_frags(t, 0, af[0], bf[0]);
 #pragma unroll
@@ -292,54 +341,47 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][i], bf[kk & 1][j], acc[i][j], 0,
                                                                       0, 0);
-            if (t + 1 < KT) {
+            // unconditional: on the last step this dequantizes the zeros
+            // loaded past K into the W stage nobody reads again
 #pragma unroll
-                for (int e = kk * E_PER_KK; e < (kk + 1) * E_PER_KK && e < W_CHUNKS; ++e) store_w_chunk(t + 1, cur, e);
+            for (int e = kk * E_PER_KK; e < (kk + 1) * E_PER_KK && e < W_CHUNKS; ++e) store_w_chunk(t + 1, cur, e);
+            // issue order: each MFMA followed by a few VALU (the dequant runs
+            // on the vector ALU while the matrix core works) and one LDS read
+#pragma unroll
+            for (int g = 0; g < TM * TN; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU
+                if (g < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        // x of step t+1 (direct-to-LDS) must have landed while the LOADS of
-        // step t+2 stay in flight (loads retire in order); the LDS writes of
-        // the dequantized W of t+1 must be done before other waves read them
-        MIQMM_WAIT_BARRIER(waitcnt_vm_lgkm0(LOADS));
+        // the x tile of step t+1 (direct-to-LDS, issued XD-1 steps ago) must
+        // have landed while the loads of the last XD-1 steps stay in flight
+        // (loads retire in order; that also covers the codes of t+2, issued
+        // WD-1 >= XD steps ago); the LDS writes of the dequantized W of t+1
+        // must be done before other waves read them
+        MIQMM_WAIT_BARRIER(waitcnt_vm_lgkm0((XD - 1) * LOADS));
     };
 
+    // The codes of step s live in wq[s % WD].  The prologue issues the loads
+    // of the steps before 0 in the loop's own order (skipping negative
+    // targets), so the loop starts with the wait counts it keeps.
+    WR wq[WD];
+#pragma unroll
+    for (int s = -WD; s < 0; ++s) {
+        load_w(s + WD, wq[s + WD]);
+        if (s + XD >= 0) issue_a(s + XD);
+    }
+    store_w(0, wq[0]);
+    MIQMM_WAIT_BARRIER(waitcnt_vm_lgkm0((XD - 1) * LOADS));  // x of step 0 and codes of step 1 landed
     int t = 0;
-#if QMM_WDIST == 2
-    WR w0, w1;
-    // same issue order as the loop, unconditionally (past K the offsets are
-    // out of range), so the loop starts with the wait counts it keeps
-    load_w(0, w0);
-    issue_a(0);
-    load_w(1, w1);
-    issue_a(1);
-    store_w(0, w0);
-    MIQMM_WAIT_BARRIER(waitcnt_vm_lgkm0(LOADS));  // x of step 0 landed
-    for (; t + 1 < KT; t += 2) {
-        step(t, w1, w0);
-        step(t + 1, w0, w1);
+    for (; t + WD - 1 < KT; t += WD) {
+#pragma unroll
+        for (int u = 0; u < WD; ++u) step(t + u, wq[(u + 1) % WD], wq[u]);
     }
-    if (t < KT) step(t, w1, w0);
-#else
-    WR w0, w1, w2;
-    // codes run three steps ahead of the MFMAs (x two): at the end of step t
-    // the wait leaves the codes of t+3 and the x of t+2 in flight, so the
-    // codes of t+2, dequantized during step t+1, have landed before it starts
-    load_w(0, w0);
-    issue_a(0);
-    load_w(1, w1);
-    load_w(2, w2);
-    issue_a(1);
-    store_w(0, w0);
-    MIQMM_WAIT_BARRIER(waitcnt_vm_lgkm0(LOADS));  // x of step 0 and codes of step 1 landed
-    for (; t + 2 < KT; t += 3) {
-        step(t, w1, w0);
-        step(t + 1, w2, w1);
-        step(t + 2, w0, w2);
-    }
-    if (t < KT) step(t, w1, w0);
-    if (t + 1 < KT) step(t + 1, w2, w1);
-#endif
+#pragma unroll
+    for (int u = 0; u + 1 < WD; ++u)
+        if (t + u < KT) step(t + u, wq[(u + 1) % WD], wq[u]);
     // the prefetches past the last step (out of range, zero-filled) still
     // write the x ring; they must land before the ring is reused below
     MIQMM_WAIT_BARRIER(0x0070);  // vmcnt(0) lgkmcnt(0)
@@ -352,7 +394,7 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
     // different banks.
     constexpr int ES = WN + 32;
     float* stage = reinterpret_cast<float*>(smem) + wid * 32 * ES;
-    const int wrow0 = m0 + wm * 128, wcol0 = n0 + wn * WN;
+    const int wrow0 = m0 + wm * WM, wcol0 = n0 + wn * WN;
     const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -410,7 +452,8 @@ __global__ __launch_bounds__(256, 1) void qmm_kernel(const uint16_t* __restrict_
 
 template <int BITS, int SBT, int BN, bool GATHER>
 hipError_t launch_t(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles) {
-    constexpr size_t lds = 3 * (size_t)kBM * kRowBytes + 2 * (size_t)BN * kRowBytes;
+    constexpr size_t lds = qmm_lds_bytes<BITS, BN>();
+    static_assert(lds <= 160 * 1024, "LDS per workgroup");
     static bool attr_set = false;  // the attribute is per kernel; setting it twice is harmless
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)qmm_kernel<BITS, SBT, BN, GATHER>,
@@ -420,7 +463,8 @@ hipError_t launch_t(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles) {
     }
     const dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)m_tiles);
     const int gs_shift = __builtin_ctz((unsigned)a.group_size);
-    hipLaunchKernelGGL((qmm_kernel<BITS, SBT, BN, GATHER>), grid, dim3(256), lds, a.stream, (const uint16_t*)a.x,
+    constexpr int threads = 64 * waves_per_block<BITS, BN>();
+    hipLaunchKernelGGL((qmm_kernel<BITS, SBT, BN, GATHER>), grid, dim3(threads), lds, a.stream, (const uint16_t*)a.x,
                        a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y, a.bias, (int)a.M, (int)a.N,
                        (int)a.K, gs_shift, a.y_dtype, gq);
     return hipGetLastError();
@@ -465,12 +509,15 @@ __global__ __launch_bounds__(1024) void gather_plan_kernel(const int32_t* idx, i
     }
 }
 
-// 256-wide tiles unless that leaves fewer tiles than CUs while 128-wide would not
+// Tile width by a rounds model: a 256-wide tile (eight waves) takes about
+// 1.4x the time of a 128-wide one (four waves) on MI355X, and tiles run in
+// rounds of one per CU (256 CUs); take the width with the smaller
+// rounds x tile time (e.g. M = 2048: 256 for N = 6144 and 14336, 128 for 4096).
 int pick_bn(int64_t M, int64_t N) {
     const int64_t mt = (M + kBM - 1) / kBM;
     const int64_t t256 = mt * ((N + 255) / 256), t128 = mt * ((N + 127) / 128);
-    if (t256 >= 256) return 256;
-    return t128 > t256 ? 128 : 256;
+    const int64_t r256 = (t256 + 255) / 256, r128 = (t128 + 255) / 256;
+    return r256 * 14 <= r128 * 10 ? 256 : 128;
 }
 
 template <int BITS, int SBT>
