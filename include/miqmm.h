@@ -200,7 +200,10 @@ int miqmm_unpack(uint8_t* codes, const uint32_t* w, int64_t N, int64_t K, int bi
  * only, no GPU access).  route_out: a miqmm_route.  tile_out[4]:
  * qmv -> {16-row tiles per block, M tile, waves per block, 0};
  * qmv_dot -> {rows per lane group, M tile, lanes per row, 0};
- * qmm -> {BM, BN, BK, 0}.
+ * qmm -> {BM, BN, BK, k ranges} (k ranges > 1: the k-steps are split over
+ * that many blocks per output tile, whose fp32 partials are summed in a
+ * library-held workspace of the stream; the unsplit kernel runs when it
+ * cannot be allocated, e.g. under stream capture).
  * No reference counterpart: reporting for benches and tests.
  */
 int miqmm_query_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, int* route_out,

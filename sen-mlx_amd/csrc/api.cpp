@@ -351,7 +351,7 @@ int miqmm_query_route(int64_t M, int64_t N, int64_t K, int group_size, int bits,
         if (route == MIQMM_ROUTE_QMV) miqmm::qmv_mfma_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
         else if (route == MIQMM_ROUTE_QMVX) miqmm::qmvx_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
         else if (route == MIQMM_ROUTE_QMV_DOT) miqmm::qmv_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
-        else miqmm::qmm_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
+        else miqmm::qmm_config(a, &tile_out[0], &tile_out[1], &tile_out[2], &tile_out[3]);
     }
     return ok();
 }

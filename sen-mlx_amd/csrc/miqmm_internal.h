@@ -74,7 +74,7 @@ bool qmvx_supported(int64_t M, int64_t K, int group_size);
 // tiling used for a given problem; for reporting
 void qmv_config(const QmmArgs& a, int* rows_per_subgroup, int* m_tile, int* lanes_per_row);
 void qmv_mfma_config(const QmmArgs& a, int* tiles_per_block, int* m_tile, int* waves_per_block);
-void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk);
+void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk, int* ks);  // ks: k ranges (split when > 1)
 void qmvx_config(const QmmArgs& a, int* m_tile, int* k_splits, int* stage_codes);
 
 hipError_t launch_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,

@@ -33,6 +33,9 @@
 //
 // Rounding the dequantized weight to bf16 before the MFMA follows MLX's qmm,
 // which dequantizes W tiles into threadgroup memory in the activation type.
+#include <algorithm>
+#include <mutex>
+
 #include "miqmm_device.h"
 #include "miqmm_internal.h"
 
@@ -119,6 +122,34 @@ struct QmmGather {
     uint32_t x_bytes;       // bytes of x (all its matrices)
 };
 
+// Split of the k-steps over gridDim.z blocks per output tile (ks > 1): each
+// block writes its fp32 partial tile to part[z], then counts itself in on
+// the tile's counter; the last block to arrive adds the other partials to
+// its own and writes the output, and resets the counter to zero.
+struct QmmSplit {
+    float* part;   // [ks][M][N] fp32 partial sums
+    int32_t* cnt;  // one arrival counter per output tile, zero between launches
+    int ks;        // number of k ranges (1: no split)
+};
+
+// fp32 partials are written and read at device scope (cache policy SC1:
+// written through to, and read from, the level coherent across the XCDs'
+// L2s), so no L2 write-back or invalidate is needed between the splits
+constexpr int kDeviceScope = 16;
+
+__device__ __forceinline__ void part_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, const f32x4_t& v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, off, 0, kDeviceScope);
+}
+__device__ __forceinline__ f32x4_t part_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kDeviceScope));
+}
+__device__ __forceinline__ void part_store1(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, kDeviceScope);
+}
+__device__ __forceinline__ float part_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kDeviceScope));
+}
+
 __device__ __forceinline__ int sload(const int32_t* p) {
     return __builtin_amdgcn_readfirstlane(*(const __attribute__((address_space(4))) int32_t*)p);
 }
@@ -149,7 +180,7 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
                                                      const uint16_t* __restrict__ bi,
                                                      void* __restrict__ y, const void* __restrict__ bias,
                                                      int M, int N, int K, int gs_shift, int y_dtype,
-                                                     const QmmGather gq) {
+                                                     const QmmGather gq, const QmmSplit sp) {
     constexpr int NW = waves_per_block<BITS, BN>(), NT = 64 * NW;
     // wave grid GM x GN: 2 x 2 for four waves; 2 x 4 (BN = 256) or 4 x 2 (BN = 128) for eight
     constexpr int GN = NW == 4 ? 2 : (BN == 256 ? 4 : 2), GM = NW / GN;
@@ -160,7 +191,7 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
     constexpr int CPR = kBK >> CPC_SHIFT;         // code chunks per W row per k-step (2 or 4)
     constexpr int W_CH = BN * CPR;                // code chunks per k-step
     constexpr int W_PER = W_CH >= NT ? W_CH / NT : 1;  // code chunks per thread (1, 2 or 4)
-    // threads past W_CH / W_PER (4-bit, BN = 128, eight waves) load out of
+    // threads from W_CH / W_PER on (4-bit, BN = 128, eight waves) load out of
     // range (zeros) and store into a dummy LDS slot, with no branch
     constexpr int XST = x_stages<BN>();           // x ring stages
     constexpr int XD = XST - 1;                   // k-steps the x tile is copied ahead
@@ -183,7 +214,13 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wid / GN, wn = wid % GN;
     const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * BN;
-    const int KT = (K + kBK - 1) / kBK;
+    // this block's k-steps: kt0 .. kt0 + KT (all of them unless split)
+    int KT = (K + kBK - 1) / kBK, kt0 = 0;
+    if (sp.ks > 1) {
+        const int chunk = (KT + sp.ks - 1) / sp.ks;
+        kt0 = blockIdx.z * chunk;
+        KT = min(KT, kt0 + chunk) - kt0;
+    }
     const uint32_t xrow = (uint32_t)K * 2;
     const uint32_t wrow = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
@@ -221,7 +258,7 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
     // of its 32-row group, stored half i%2, so it loads logical half
     // (i%2) ^ (bit 3 of the row)
     auto issue_a = [&](int kt) {
-        const int kb = kt * kBK + xslice * 16;
+        const int kb = (kt0 + kt) * kBK + xslice * 16;
         char* slice = smem + (kt % XST) * A_STAGE + xslice * kBM * 32 + xrow0 * 32;
 #pragma unroll
         for (int j = 0; j < XI; ++j) {
@@ -235,14 +272,17 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
         }
     };
 
-    // this thread's W row and first code chunk
+    // this thread's W row and first code chunk (adjacent lanes share a row:
+    // the code loads of a wave cover 32-byte runs of 32 rows; mapping
+    // consecutive lanes to consecutive rows instead, which makes the LDS
+    // stores below conflict-free, measured 15 % slower on MI355X)
     const int wrow_t = tid / (CPR / W_PER);
     const int wch0 = (tid % (CPR / W_PER)) * W_PER;
     const bool widle = tid >= W_CH / W_PER;
     const uint32_t wid_oob = widle ? kOOB : 0u;
     using WR = WRegs<BITS, W_PER>;
     auto load_w = [&](int kt, WR& r) {
-        const int kb = kt * kBK;
+        const int kb = (kt0 + kt) * kBK;
 #pragma unroll
         for (int i = 0; i < W_PER; ++i) {
             const int kc = kb + ((wch0 + i) << CPC_SHIFT);
@@ -396,62 +436,144 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
     float* stage = reinterpret_cast<float*>(smem) + wid * 32 * ES;
     const int wrow0 = m0 + wm * WM, wcol0 = n0 + wn * WN;
     const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    constexpr int FLAG = (int)qmm_lds_bytes<BITS, BN>() - 16;  // LDS word for the last-arrival flag
+    static_assert(NW * 32 * ES * 4 <= FLAG, "epilogue staging below the flag");
+    // unsplit: the output; split: this block's fp32 partial tile -> part[z]
+    const bool partial = sp.ks > 1;
+    {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+        for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                stage[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ES + j * 32 + (lane & 31)] = acc[i][j][r];
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
-        __builtin_amdgcn_wave_barrier();
-        constexpr int RUNS = WN / 8;
+                for (int r = 0; r < 16; ++r)
+                    stage[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ES + j * 32 + (lane & 31)] = acc[i][j][r];
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+            __builtin_amdgcn_wave_barrier();
+            constexpr int RUNS = WN / 8;
 #pragma unroll 1
-        for (int p = lane; p < 32 * RUNS; p += 64) {
-            const int row = p / RUNS, c8 = p % RUNS;
-            int gr = wrow0 + i * 32 + row;
-            const int gc = wcol0 + c8 * 8;
-            if constexpr (GATHER) {  // the tile's row -> its selection, one output row each
-                const int lr = gr - m0;
-                if (lr >= mrows || gc >= N) continue;
-                gr = gq.perm[p0 + lr];
-            } else {
-                if (gr >= M || gc >= N) continue;
+            for (int p = lane; p < 32 * RUNS; p += 64) {
+                const int row = p / RUNS, c8 = p % RUNS;
+                int gr = wrow0 + i * 32 + row;
+                const int gc = wcol0 + c8 * 8;
+                if constexpr (GATHER) {  // the tile's row -> its selection, one output row each
+                    const int lr = gr - m0;
+                    if (lr >= mrows || gc >= N) continue;
+                    gr = gq.perm[p0 + lr];
+                } else {
+                    if (gr >= M || gc >= N) continue;
+                }
+                f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(stage + row * ES + c8 * 8);
+                f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(stage + row * ES + c8 * 8 + 4);
+                const int64_t o = (int64_t)gr * N + gc;
+                const uint32_t po = (uint32_t)o * 4;  // byte offset in one split's partials
+                if (partial) {
+                    const auto pr = make_rsrc(sp.part + (int64_t)blockIdx.z * M * N, (uint32_t)M * N * 4);
+                    if (vec) {
+                        part_store4(pr, po, v0);
+                        part_store4(pr, po + 16, v1);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            if (gc + e < N) part_store1(pr, po + 4 * e, e < 4 ? v0[e] : v1[e - 4]);
+                    }
+                    continue;
+                }
+                const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                if (vec && y_dtype != DT_F32) {  // gc + 8 <= N since N % 8 == 0
+                    u32x4_t h;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        h[e] = (uint32_t)out_half_bits(y_dtype, v[2 * e], bias, gc + 2 * e) |
+                               ((uint32_t)out_half_bits(y_dtype, v[2 * e + 1], bias, gc + 2 * e + 1) << 16);
+                    *reinterpret_cast<u32x4_t*>((uint16_t*)y + o) = h;
+                } else if (vec) {
+                    f32x4_t a = v0, b = v1;
+                    if (bias) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            a[e] += ((const float*)bias)[gc + e];
+                            b[e] += ((const float*)bias)[gc + 4 + e];
+                        }
+                    }
+                    *reinterpret_cast<f32x4_t*>((float*)y + o) = a;
+                    *reinterpret_cast<f32x4_t*>((float*)y + o + 4) = b;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (gc + e < N) store_out(y, o + e, y_dtype, v[e], bias, gc + e);
+                }
             }
-            const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(stage + row * ES + c8 * 8);
-            const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(stage + row * ES + c8 * 8 + 4);
-            const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            __builtin_amdgcn_wave_barrier();  // reads of this band before the next band's writes
+        }
+    }
+    if (!partial) return;
+    // every partial store of this block has completed (device-scope stores
+    // count in vmcnt until they reach the coherent level), then count in
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    __syncthreads();
+    int* flag = reinterpret_cast<int*>(smem + FLAG);
+    if (tid == 0) {
+        int32_t* c = sp.cnt + blockIdx.y * gridDim.x + blockIdx.x;
+        const int last = atomicAdd(c, 1) == sp.ks - 1;
+        if (last) *c = 0;  // every split has counted in: ready for the next launch
+        *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return;  // block-uniform
+    // the last block to arrive sums the ks partials of the tile in split
+    // order (the same result whichever block is last) and writes the output;
+    // four runs of 8 outputs per thread in flight at a time
+    constexpr int RUNS_T = BN / 8;
+    const auto pr = make_rsrc(sp.part, (uint32_t)min((int64_t)sp.ks * M * N * 4, (int64_t)0xFFFFFFF0));
+#pragma unroll 1
+    for (int q0 = tid; q0 < kBM * RUNS_T; q0 += 4 * NT) {
+        f32x4_t a0[4], a1[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a0[u] = a1[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (int z = 0; z < sp.ks; ++z) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int q = q0 + u * NT, gr = m0 + q / RUNS_T, gc = n0 + (q % RUNS_T) * 8;
+                if (q >= kBM * RUNS_T || gr >= M || gc >= N) continue;
+                const uint32_t po = (uint32_t)(((int64_t)z * M * N + (int64_t)gr * N + gc) * 4);
+                if (vec) {
+                    a0[u] += part_load4(pr, po);
+                    a1[u] += part_load4(pr, po + 16);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (gc + e < N) a0[u][e] += part_load1(pr, po + 4 * e);
+                        if (gc + 4 + e < N) a1[u][e] += part_load1(pr, po + 16 + 4 * e);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = q0 + u * NT, gr = m0 + q / RUNS_T, gc = n0 + (q % RUNS_T) * 8;
+            if (q >= kBM * RUNS_T || gr >= M || gc >= N) continue;
             const int64_t o = (int64_t)gr * N + gc;
-            if (vec && y_dtype != DT_F32) {  // gc + 8 <= N since N % 8 == 0
+            const float v[8] = {a0[u][0], a0[u][1], a0[u][2], a0[u][3], a1[u][0], a1[u][1], a1[u][2], a1[u][3]};
+            if (vec && y_dtype != DT_F32) {
                 u32x4_t h;
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     h[e] = (uint32_t)out_half_bits(y_dtype, v[2 * e], bias, gc + 2 * e) |
                            ((uint32_t)out_half_bits(y_dtype, v[2 * e + 1], bias, gc + 2 * e + 1) << 16);
                 *reinterpret_cast<u32x4_t*>((uint16_t*)y + o) = h;
-            } else if (vec) {
-                f32x4_t a = v0, b = v1;
-                if (bias) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        a[e] += ((const float*)bias)[gc + e];
-                        b[e] += ((const float*)bias)[gc + 4 + e];
-                    }
-                }
-                *reinterpret_cast<f32x4_t*>((float*)y + o) = a;
-                *reinterpret_cast<f32x4_t*>((float*)y + o + 4) = b;
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
                     if (gc + e < N) store_out(y, o + e, y_dtype, v[e], bias, gc + e);
             }
         }
-        __builtin_amdgcn_wave_barrier();  // reads of this band before the next band's writes
     }
 }
 
 template <int BITS, int SBT, int BN, bool GATHER>
-hipError_t launch_t(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles) {
+hipError_t launch_t(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles, const QmmSplit& sp) {
     constexpr size_t lds = qmm_lds_bytes<BITS, BN>();
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
     static bool attr_set = false;  // the attribute is per kernel; setting it twice is harmless
@@ -461,12 +583,12 @@ hipError_t launch_t(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles) {
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    const dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)m_tiles);
+    const dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)m_tiles, (unsigned)sp.ks);
     const int gs_shift = __builtin_ctz((unsigned)a.group_size);
     constexpr int threads = 64 * waves_per_block<BITS, BN>();
     hipLaunchKernelGGL((qmm_kernel<BITS, SBT, BN, GATHER>), grid, dim3(threads), lds, a.stream, (const uint16_t*)a.x,
                        a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y, a.bias, (int)a.M, (int)a.N,
-                       (int)a.K, gs_shift, a.y_dtype, gq);
+                       (int)a.K, gs_shift, a.y_dtype, gq, sp);
     return hipGetLastError();
 }
 
@@ -509,39 +631,125 @@ __global__ __launch_bounds__(1024) void gather_plan_kernel(const int32_t* idx, i
     }
 }
 
-// Tile width by a rounds model: a 256-wide tile (eight waves) takes about
-// 1.4x the time of a 128-wide one (four waves) on MI355X, and tiles run in
-// rounds of one per CU (256 CUs); take the width with the smaller
-// rounds x tile time (e.g. M = 2048: 256 for N = 6144 and 14336, 128 for 4096).
-int pick_bn(int64_t M, int64_t N) {
-    const int64_t mt = (M + kBM - 1) / kBM;
-    const int64_t t256 = mt * ((N + 255) / 256), t128 = mt * ((N + 127) / 128);
-    const int64_t r256 = (t256 + 255) / 256, r128 = (t128 + 255) / 256;
-    return r256 * 14 <= r128 * 10 ? 256 : 128;
+// Tile width and k split by a rounds model of MI355X: tiles run in rounds
+// of one block per CU (256 CUs); a 128-wide tile (four waves) over K takes
+// about 0.0202 us per unit of K, a 256-wide one (eight waves) 1.3x that; a
+// split into ks k ranges divides the tile time by ks and adds the partial
+// traffic, (2 ks - 1) fp32 values per output at a measured 1.6 TB/s
+// effective.  E.g. M = 2048: N = 14336 and 6144 -> 256 wide, N = 4096 ->
+// 128 wide at K = 4096 and 256 wide in two k ranges at K = 14336; M = 256,
+// N = 4096, K = 4096 -> 128 wide in four k ranges.
+struct QmmPlan {
+    int bn, ks;
+};
+
+QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int max_ks) {
+    const int64_t mt = (M + kBM - 1) / kBM, KT = (K + kBK - 1) / kBK;
+    QmmPlan best{128, 1};
+    double best_us = 1e300;
+    for (int bn : {128, 256}) {
+        const int64_t tiles = mt * ((N + bn - 1) / bn);
+        for (int ks = 1; ks <= max_ks; ++ks) {
+            if (ks > 1 && (KT < 8 * ks || (double)ks * M * N * 4 >= 2147483648.0)) break;  // >= 8 k-steps per range
+            const double rounds = (double)((tiles * ks + 255) / 256);
+            double us = rounds * (bn == 256 ? 1.3 : 1.0) * 0.0202 * (double)K / ks;
+            if (ks > 1) us += (double)M * N * 4 * (2 * ks - 1) / 1.6e6;
+            if (us < best_us) {
+                best_us = us;
+                best = {bn, ks};
+            }
+        }
+    }
+    return best;
+}
+
+constexpr int kMaxSplit = 4;
+
+// The split path's device workspace per (device, stream): tile counters
+// (zero between launches: each tile's last block resets its own) followed by
+// the fp32 partials.  Allocated or grown only outside stream capture; when
+// it cannot be had the caller runs unsplit.  One table entry per stream, so
+// calls on different streams never share counters or partials.
+struct SplitWs {
+    int device;
+    hipStream_t stream;
+    char* ptr;
+    size_t cnt_bytes, part_bytes;
+};
+std::mutex g_split_mu;
+SplitWs g_split[8];
+int g_split_n = 0;
+
+bool split_workspace(hipStream_t stream, size_t cnt_bytes, size_t part_bytes, QmmSplit& sp) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return false;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    std::lock_guard<std::mutex> lock(g_split_mu);
+    SplitWs* e = nullptr;
+    for (int i = 0; i < g_split_n; ++i)
+        if (g_split[i].device == dev && g_split[i].stream == stream) e = &g_split[i];
+    if (!e || e->cnt_bytes < cnt_bytes || e->part_bytes < part_bytes) {
+        if (cs != hipStreamCaptureStatusNone) return false;
+        if (!e) {
+            if (g_split_n == 8) return false;
+            e = &g_split[g_split_n++];
+            *e = {dev, stream, nullptr, 0, 0};
+        }
+        if (e->ptr) {  // the old buffer may still be in use by this stream's kernels
+            if (hipStreamSynchronize(stream) != hipSuccess) return false;
+            (void)hipFree(e->ptr);
+            e->ptr = nullptr;
+        }
+        const size_t cb = (std::max(cnt_bytes, e->cnt_bytes) + 255) / 256 * 256;
+        const size_t pb = (std::max(part_bytes, e->part_bytes) + 255) / 256 * 256;
+        e->cnt_bytes = e->part_bytes = 0;
+        if (hipMalloc(&e->ptr, cb + pb) != hipSuccess) {
+            e->ptr = nullptr;
+            (void)hipGetLastError();
+            return false;
+        }
+        if (hipMemsetAsync(e->ptr, 0, cb, stream) != hipSuccess) return false;
+        e->cnt_bytes = cb;
+        e->part_bytes = pb;
+    }
+    sp.cnt = reinterpret_cast<int32_t*>(e->ptr);
+    sp.part = reinterpret_cast<float*>(e->ptr + e->cnt_bytes);
+    return true;
 }
 
 template <int BITS, int SBT>
 hipError_t launch_bn(const QmmArgs& a) {
     const QmmGather none{};
     const int64_t mt = (a.M + kBM - 1) / kBM;
-    return pick_bn(a.M, a.N) == 256 ? launch_t<BITS, SBT, 256, false>(a, none, mt)
-                                    : launch_t<BITS, SBT, 128, false>(a, none, mt);
+    QmmPlan pl = plan_qmm(a.M, a.N, a.K, kMaxSplit);
+    QmmSplit sp{nullptr, nullptr, 1};
+    if (pl.ks > 1) {
+        const int64_t tiles = mt * ((a.N + pl.bn - 1) / pl.bn);
+        if (split_workspace(a.stream, (size_t)tiles * 4, (size_t)pl.ks * a.M * a.N * 4, sp)) sp.ks = pl.ks;
+        else pl = plan_qmm(a.M, a.N, a.K, 1);
+    }
+    return pl.bn == 256 ? launch_t<BITS, SBT, 256, false>(a, none, mt, sp)
+                        : launch_t<BITS, SBT, 128, false>(a, none, mt, sp);
 }
 
 template <int BITS, int SBT>
 hipError_t launch_gather_bn(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles) {
     // the expert-grouped grid has as many M tiles as experts or more: 128-wide
     // tiles fill the chip whenever 256-wide ones would not
-    return pick_bn(kBM * m_tiles, a.N) == 256 ? launch_t<BITS, SBT, 256, true>(a, gq, m_tiles)
-                                               : launch_t<BITS, SBT, 128, true>(a, gq, m_tiles);
+    const QmmSplit unsplit{nullptr, nullptr, 1};
+    return plan_qmm(kBM * m_tiles, a.N, a.K, 1).bn == 256 ? launch_t<BITS, SBT, 256, true>(a, gq, m_tiles, unsplit)
+                                                         : launch_t<BITS, SBT, 128, true>(a, gq, m_tiles, unsplit);
 }
 
 }  // namespace
 
-void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk) {
+void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk, int* ks) {
+    const QmmPlan pl = plan_qmm(a.M, a.N, a.K, kMaxSplit);
     if (bm) *bm = kBM;
-    if (bn) *bn = pick_bn(a.M, a.N);
+    if (bn) *bn = pl.bn;
     if (bk) *bk = kBK;
+    if (ks) *ks = pl.ks;
 }
 
 hipError_t launch_qmm(const QmmArgs& a) {
