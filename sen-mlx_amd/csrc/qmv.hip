@@ -16,8 +16,9 @@
 //
 // Waves are persistent: a wave walks row tiles tile, tile+nwaves, ... and the
 // (tile, chunk) iterations are software-pipelined one deep: the next
-// iteration's codes, scales, biases and x are in flight while the current one
-// is computed, so a wave keeps ~R*16 bytes per lane outstanding at all times.
+// iteration's codes, scales, biases (and x, unless the block holds x in its
+// LDS table) are in flight while the current one is computed, so a wave keeps
+// ~R*16 bytes per lane outstanding at all times.
 //
 // Arithmetic: codes become exact bf16 operands (4-bit: 0x4300|q = 128+q;
 // 8-bit: the top half of the fp32 value of q) and are dotted with x by
@@ -74,16 +75,38 @@ struct TileRef {
     int N, row0, rows;   // problem rows, first row of the tile, rows present (0: read nothing)
 };
 
+// bytes of dynamic LDS the x table of one row of x takes: the prepared x
+// words of every chunk (plus a zero chunk for lanes past the row end), then
+// each chunk's sum of x
+int64_t x_table_bytes(int64_t K, int bits) {
+    const int64_t C = K * bits / 128, NP = (128 / bits) / 2;
+    return (C + 1) * NP * 4 + (C + 1) * 4;
+}
+constexpr int64_t kMaxXTable = 64 * 1024;
+// Rows shorter than this, and split tiles, keep the per-stage x: their
+// blocks are short-lived and the table's build (an x load, then a barrier,
+// before the first code load) is exposed (measured on MI355X: the 0.5B
+// decode step 367 -> 389 us with the table on every shape, 378 with it on
+// the split 4864 -> 896 projections only).
+constexpr int64_t kMinXTableK = 2048;
+
 // MODE 0: P holds one problem (every lookup folds to problem 0 at compile
-// time); 1: P.count problems, grouped; 2: expert gather
-template <int BITS, int SBT, int MT, int L, int R, int MODE>
+// time); 1: P.count problems, grouped; 2: expert gather.
+// XL (one row of x shared by every problem): the block prepares x once into
+// an LDS table at start (the pairing the code unpack needs and each chunk's
+// sum of x), and the stages read their chunk from it; otherwise every stage
+// loads its x chunk and prepares it again.  The same arithmetic on the same
+// values either way: the results are identical bit for bit.
+template <int BITS, int SBT, int MT, int L, int R, int MODE, bool XL = false>
 __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, int K, int gs_shift, int y_dtype) {
     constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk: 32 or 16
     constexpr int CPC = 1 << CPC_SHIFT;
     constexpr int NP = CPC / 2;
+    constexpr int NQ = NP / 4;                    // 16-byte quads of prepared x per chunk
     constexpr int SG = 64 / L;                    // sub-groups (row slots) per wave
     constexpr int TILE = SG * R;                  // rows per wave tile
-    constexpr bool XPF = MT <= 2;                 // prefetch x with the codes (registers allow it)
+    constexpr bool XPF = MT <= 2 && !XL;          // prefetch x with the codes (registers allow it)
+    static_assert(!XL || (MT == 1 && MODE != 2), "x table: one shared row of x");
     using St = Stage<BITS, R, MT, XPF>;
 
     const int lane = threadIdx.x & 63;
@@ -114,7 +137,11 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     const int j_count = ks ? (wv + 1) * J / 4 - j_begin : J;
     const int my_tiles = tile_first < tiles ? (tiles - 1 - tile_first) / tile_stride + 1 : 0;
     const int iters = my_tiles * j_count;
-    if (iters == 0) return;  // uniform over the block when ksplit (J >= 4 gives every wave chunks)
+    // x table: quad q of chunk c at quad c*NQ + (q + (c >> ROT)) % NQ, so the
+    // quads that 16 lanes read from 16 consecutive chunks cover all 64 banks;
+    // the chunk sums follow
+    extern __shared__ u32x4_t xtab[];
+    constexpr int ROT = NQ == 4 ? 2 : 3;  // chunks per 256 bytes: 4 or 8
     __shared__ float kpart[2][4][64];  // ksplit partial sums, double-buffered by tile parity
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
@@ -212,7 +239,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
             st.s[r] = bload2(sr, (row * G + g) * 2);
             st.b[r] = bload2(br, (row * G + g) * 2);
         }
-        st.xoff = cv ? (uint32_t)c * CPC * 2 : kOOB;
+        if constexpr (XL) st.xoff = cv ? (uint32_t)c : (uint32_t)C;  // the zero chunk past the row end
+        else st.xoff = cv ? (uint32_t)c * CPC * 2 : kOOB;
         if constexpr (XPF) load_x(make_rsrc(t.x, (uint32_t)M * xrow_bytes), st.xoff, st.xw);
     };
 
@@ -225,7 +253,18 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     auto compute = [&](const St& st) {
         uint32_t X[MT][NP];
         float xs[MT];
-        if constexpr (XPF) {
+        if constexpr (XL) {
+            const int c = (int)st.xoff;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const u32x4_t v = xtab[c * NQ + ((q + (c >> ROT)) & (NQ - 1))];
+                X[0][4 * q + 0] = v[0];
+                X[0][4 * q + 1] = v[1];
+                X[0][4 * q + 2] = v[2];
+                X[0][4 * q + 3] = v[3];
+            }
+            xs[0] = reinterpret_cast<const float*>(xtab + (C + 1) * NQ)[c];
+        } else if constexpr (XPF) {
             prep_x(st.xw, X, xs);
         } else {
             uint32_t xw[MT][NP];
@@ -299,10 +338,51 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     };
 
     // one-deep software pipeline over (tile, chunk) iterations, ping-ponging
-    // between two stages so no stage is ever copied
+    // between two stages so no stage is ever copied.  Without the x table the
+    // first two stages are issued first thing (measured 3 % faster on the
+    // 0.5B decode step than after the early exit); with it the table is
+    // built first (issuing the code loads before it was 5 % slower: the
+    // table's x loads then return behind the codes).
     St A, B;
-    issue(A);
-    if (iters > 1) issue(B);
+    if constexpr (!XL) {
+        if (iters > 0) issue(A);
+        if (iters > 1) issue(B);
+    }
+    if constexpr (XL) {  // build the x table
+        float* const xsum = reinterpret_cast<float*>(xtab + (C + 1) * NQ);
+        const auto xr = make_rsrc(P.p[0].x, (uint32_t)K * 2);
+        for (int c = threadIdx.x; c <= C; c += blockDim.x) {
+            uint32_t xw[NP], X[NP];
+#pragma unroll
+            for (int i = 0; i < NQ; ++i) {
+                const u32x4_t v = bload16(xr, c < C ? (uint32_t)c * CPC * 2 + i * 16 : kOOB);
+                xw[4 * i + 0] = v[0];
+                xw[4 * i + 1] = v[1];
+                xw[4 * i + 2] = v[2];
+                xw[4 * i + 3] = v[3];
+            }
+            float xs = 0.f;
+#pragma unroll
+            for (int i = 0; i < NP; ++i) xs = dot2(xw[i], kOnesBf16x2, xs);
+            if constexpr (BITS == 4) {
+#pragma unroll
+                for (int wi = 0; wi < 4; ++wi) perm_x_for4(&xw[4 * wi], &X[4 * wi]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < NP; ++i) X[i] = xw[i];
+            }
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+                xtab[c * NQ + ((q + (c >> ROT)) & (NQ - 1))] = u32x4_t{X[4 * q], X[4 * q + 1], X[4 * q + 2], X[4 * q + 3]};
+            xsum[c] = xs;
+        }
+        __syncthreads();  // every wave of the block, before any of them may return
+    }
+    if (iters == 0) return;  // uniform over the block when ksplit (J >= 4 gives every wave chunks)
+    if constexpr (XL) {
+        issue(A);
+        if (iters > 1) issue(B);
+    }
     for (int it = 0; it < iters; it += 2) {
         if (it > 0 && it + 1 < iters) issue(B);
         compute(A);
@@ -345,6 +425,20 @@ hipError_t launch_t(const QmmArgs* a, int count) {
     P.ksplit = use_ksplit(tiles, a[0].K, a[0].bits, L);
     const int blocks = gemv_blocks(tiles, P.ksplit);
     const int gs_shift = __builtin_ctz((unsigned)a[0].group_size);
+    if constexpr (MT == 1) {  // one row of x shared by every problem: the LDS x table
+        bool shared = true;
+        for (int i = 1; i < count; ++i) shared = shared && a[i].x == a[0].x;
+        const int64_t xt = x_table_bytes(a[0].K, BITS);
+        if (shared && !P.ksplit && a[0].K >= kMinXTableK && xt <= kMaxXTable) {
+            if (count > 1)
+                hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 1, true>), dim3(blocks), dim3(256), (size_t)xt,
+                                   a[0].stream, P, (int)a[0].M, (int)a[0].K, gs_shift, a[0].y_dtype);
+            else
+                hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 0, true>), dim3(blocks), dim3(256), (size_t)xt,
+                                   a[0].stream, P, (int)a[0].M, (int)a[0].K, gs_shift, a[0].y_dtype);
+            return hipGetLastError();
+        }
+    }
     if constexpr (MT <= 2) {
         if (count > 1) {
             hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 1>), dim3(blocks), dim3(256), 0, a[0].stream, P,
