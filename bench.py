@@ -246,7 +246,7 @@ def moe_and_embedding(miqmm, torch):
         gate = [t.reshape(E, I, -1) for t in miqmm.synth_problem(1, E * I, H, g, 4, seed=60 + r, stream_id=1)[1:]]
         down = [t.reshape(E, H, -1) for t in miqmm.synth_problem(1, E * H, I, g, 4, seed=70 + r, stream_id=2)[1:]]
         stacks.append((gate, down))
-    for T in (1, 64, 1024):
+    for T in (1, 16, 64, 1024):
         gen = torch.Generator().manual_seed(T)
         idx = torch.stack([torch.randperm(E, generator=gen)[:top_k] for _ in range(T)]).to(torch.int32).cuda()
         x = torch.randn(T, 1, 1, H, device="cuda").to(torch.bfloat16)
@@ -258,14 +258,18 @@ def moe_and_embedding(miqmm, torch):
                        n, 5)
         td = graph_avg(torch, [lambda s=s: miqmm.gather_qmm(h, *s[1], idx, True, g, 4, out=yd) for s in stacks],
                        n, 5)
-        sel = T * top_k * qbytes(1, I, H)  # bytes of the selected experts (each selection streams its expert)
         fl = 2 * T * top_k * H * I
-        grouped = T * top_k >= 8 * E
+        S = T * top_k
+        path = ("expert-grouped tiled matmul" if S >= miqmm.GROUPED_MIN_PER_EXPERT * E else
+                "expert-grouped MFMA GEMV" if S >= miqmm.GROUPED_GEMV_MIN_PER_EXPERT * E else
+                "per-selection v_dot2 GEMV")
+        # bytes the path must stream: each selection's expert (per-selection),
+        # or each distinct selected expert once (grouped)
+        streams = S if path.startswith("per-selection") else len(set(idx.flatten().tolist()))
+        nb = streams * qbytes(1, I, H)
         res[f"gather_qmm_T{T}"] = {"gate_2048to1408_us": round(tg * 1e6, 2), "down_1408to2048_us": round(td * 1e6, 2),
-                                   "gate_TFLOP/s": round(fl / tg / 1e12, 1),
-                                   "path": "expert-grouped tiled matmul" if grouped else "per-selection v_dot2 GEMV"}
-        if not grouped:  # every selection streams its expert: that is the byte count
-            res[f"gather_qmm_T{T}"].update({"selected_expert_bytes": sel, "gate_GB/s": round(sel / tg / 1e9, 1)})
+                                   "gate_TFLOP/s": round(fl / tg / 1e12, 1), "path": path,
+                                   "weight_bytes": nb, "gate_GB/s": round(nb / tg / 1e9, 1)}
     del stacks
     V, K = 151936, 896
     tabs = [miqmm.synth_problem(1, V, K, g, 4, seed=80 + r, stream_id=3)[1:] for r in range(3)]

@@ -159,10 +159,12 @@ int miqmm_dequantize(void* out, const uint32_t* w, const void* scales, const voi
 /*
  * miqmm_gather_qmm with a caller-provided device workspace (16-byte aligned,
  * at least miqmm_gather_qmm_workspace_size bytes).  With M == 1 and enough
- * selections per expert (prefill-sized batches), the selections are grouped
- * by expert on the device and each expert's weights are streamed once through
- * the tiled MFMA matmul (the qmm route's arithmetic: W rounded to bf16 after
- * the fp32 dequant) instead of once per selection; otherwise, or without a
+ * selections per expert, the selections are grouped by expert on the device
+ * and each selected expert's weights are streamed once instead of once per
+ * selection: from 8 selections per expert on average (prefill-sized batches)
+ * through the tiled MFMA matmul (the qmm route's arithmetic: W rounded to
+ * bf16 after the fp32 dequant), from 4 through the MFMA GEMV, 16 selections
+ * per tile (exact fp32 dequant, as the GEMV routes); otherwise, or without a
  * workspace, this is miqmm_gather_qmm.  No counterpart in the reference (its
  * wrapper, src/engine/mlx_lm/utils/moe.rs:33-77, always passes
  * sorted_indices=false): the caller that can pass scratch memory for it.

@@ -41,6 +41,14 @@ constexpr int64_t kMaxDim = (int64_t)1 << 31;
 #define MIQMM_GROUPED_MIN 8
 #endif
 constexpr int64_t kGroupedMinPerExpert = MIQMM_GROUPED_MIN;
+// ... and into the grouped MFMA GEMV (fewer selections per expert; below
+// about 4 the per-selection GEMV, which streams some experts several times
+// but at a higher rate, is faster: DeepSeek-V2-Lite gate/down at 16 tokens
+// 39/38 us per-selection vs 67/51 grouped, at 64 tokens 136/134 vs 83/64)
+#ifndef MIQMM_GROUPED_GEMV_MIN
+#define MIQMM_GROUPED_GEMV_MIN 4
+#endif
+constexpr int64_t kGroupedGemvMinPerExpert = MIQMM_GROUPED_GEMV_MIN;
 
 int check_quant(int64_t N, int64_t K, int group_size, int bits, int sb_dtype) {
     if (bits != 4 && bits != 8) {
@@ -165,14 +173,22 @@ int gather_common(void* y, const void* x, const uint32_t* w, const void* scales,
     if (!rhs_indices) return fail(MIQMM_EINVAL, "null pointer argument");
     if (problems * M * (K > N ? K : N) >= ((int64_t)1 << 40)) return fail(MIQMM_EINVAL, "batch*top_k*M*K too large");
     const int64_t x_bytes = (x_per_index ? problems : batch) * M * K * 2;
-    if (workspace && M == 1 && problems >= kGroupedMinPerExpert * experts && experts <= 1024 &&
+    // with a workspace and one row of x per selection, the selections are
+    // grouped by expert so each selected expert's weights stream once: on the
+    // tiled MFMA matmul when there are many selections per expert, on the
+    // MFMA GEMV (16 selections per tile) from 4 selections per expert
+    if (workspace && M == 1 && problems >= kGroupedGemvMinPerExpert * experts && experts <= 1024 &&
         x_bytes < ((int64_t)1 << 31) && workspace_bytes >= miqmm::gather_grouped_workspace(problems, experts)) {
         if (!aligned16(workspace)) return fail(MIQMM_EINVAL, "workspace must be 16-byte aligned");
         miqmm::QmmArgs a{y, x, w, scales, biases, nullptr, problems, N, K, group_size, bits, x_dtype, sb_dtype,
                          y_dtype, reinterpret_cast<hipStream_t>(stream)};
-        return check_launch(miqmm::launch_gather_grouped(a, rhs_indices, batch, (int)top_k, x_per_index, experts,
-                                                          x_bytes, workspace),
-                            "grouped gather launch");
+        if (problems >= kGroupedMinPerExpert * experts)
+            return check_launch(miqmm::launch_gather_grouped(a, rhs_indices, batch, (int)top_k, x_per_index,
+                                                              experts, x_bytes, workspace),
+                                "grouped gather launch");
+        return check_launch(miqmm::launch_gather_gemv(a, rhs_indices, batch, (int)top_k, x_per_index, experts,
+                                                       x_bytes, workspace),
+                            "grouped gather GEMV launch");
     }
     // the GEMV handles 16 rows of x per pass over a weight tile; more rows
     // (rare in decode) take several passes, one per 16-row slice of every matrix

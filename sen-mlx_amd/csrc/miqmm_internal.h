@@ -61,13 +61,30 @@ hipError_t launch_qmv_gather(const QmmArgs& a, const int32_t* idx, int64_t T, in
                              int64_t experts, int64_t x_stride, int64_t y_stride);
 hipError_t launch_qmv_mfma(const QmmArgs& a);  // group-diagonal MFMA GEMV
 hipError_t launch_qmm(const QmmArgs& a);
-// expert-grouped gather_qmm on the tiled MFMA matmul (M = 1 per selection):
-// a describes expert 0 (w / scales / biases bases, N, K); T * top_k
-// selections; the workspace holds the grouping (gather_grouped_workspace bytes)
-int64_t gather_grouped_max_tiles(int64_t S, int64_t E);
-int64_t gather_grouped_workspace(int64_t S, int64_t E);
+// expert grouping of gather_qmm's selections (M = 1 per selection): the
+// workspace (gather_grouped_workspace bytes) holds, per expert, its range of
+// the selection list, and the list of tiles of up to `tr` selections of one
+// expert.  a describes expert 0 (w / scales / biases bases, N, K); T * top_k
+// selections.  Two consumers: the tiled MFMA matmul (tiles of 256 rows, for
+// prefill-sized batches) and the MFMA GEMV (tiles of 16 rows, for batches
+// with a few selections per expert).
+constexpr int kGatherGemvRows = 16;  // selections per tile of the grouped MFMA GEMV
+struct GatherPlan {
+    int32_t* seg;     // [E + 2]: expert e's range of perm is seg[e] .. seg[e+1] (e == E: invalid ids)
+    int32_t* ntiles;  // number of tiles
+    int32_t* perm;    // [S] selection ids grouped by expert
+    int32_t* tiles;   // [max tiles][2]: (expert, first position in perm)
+    int64_t max_tiles;
+};
+int64_t gather_grouped_max_tiles(int64_t S, int64_t E, int tr);
+int64_t gather_grouped_workspace(int64_t S, int64_t E);  // enough for either consumer
+GatherPlan gather_plan_layout(void* workspace, int64_t S, int64_t E, int tr);
+hipError_t launch_gather_plan(const int32_t* idx, int64_t S, int64_t E, int tr, const GatherPlan& plan,
+                              hipStream_t stream);
 hipError_t launch_gather_grouped(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_index,
                                  int64_t experts, int64_t x_bytes, void* workspace);
+hipError_t launch_gather_gemv(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_index,
+                              int64_t experts, int64_t x_bytes, void* workspace);
 hipError_t launch_qmvx(const QmmArgs& a);      // MFMA GEMV, M <= 4, x in LDS
 bool qmvx_supported(int64_t M, int64_t K, int group_size);
 

@@ -592,13 +592,13 @@ hipError_t launch_t(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles, cons
     return hipGetLastError();
 }
 
-// One block groups the selections by expert for the expert-grouped matmul:
+// One block groups the selections by expert for the expert-grouped kernels:
 // a histogram of the indices in LDS, its prefix sum (the experts' ranges of
 // the selection list; ids outside [0, E) form range E), the selections
-// placed into their ranges, and the list of 256-row M tiles.  The order of
-// selections inside a range is arbitrary; every output row is computed on its
-// own, so the results do not depend on it.
-__global__ __launch_bounds__(1024) void gather_plan_kernel(const int32_t* idx, int S, int E, int32_t* seg,
+// placed into their ranges, and the list of tiles of up to `tr` rows.  The
+// order of selections inside a range is arbitrary; every output row is
+// computed on its own, so the results do not depend on it.
+__global__ __launch_bounds__(1024) void gather_plan_kernel(const int32_t* idx, int S, int E, int tr, int32_t* seg,
                                                            int32_t* ntiles, int32_t* perm, int32_t* tiles) {
     extern __shared__ int32_t cnt[];  // [E + 1] counts, then [E + 1] fill positions
     int32_t* pos = cnt + E + 1;
@@ -614,7 +614,7 @@ __global__ __launch_bounds__(1024) void gather_plan_kernel(const int32_t* idx, i
         for (int e = 0; e <= E; ++e) {
             seg[e] = run;
             pos[e] = run;
-            for (int r = 0; r < cnt[e]; r += kBM) {
+            for (int r = 0; r < cnt[e]; r += tr) {
                 tiles[2 * t] = e;
                 tiles[2 * t + 1] = run + r;
                 ++t;
@@ -757,26 +757,38 @@ hipError_t launch_qmm(const QmmArgs& a) {
     return a.sb_dtype == DT_F16 ? launch_bn<8, DT_F16>(a) : launch_bn<8, DT_BF16>(a);
 }
 
+int64_t gather_grouped_max_tiles(int64_t S, int64_t E, int tr) { return S / tr + E + 1; }
+
 int64_t gather_grouped_workspace(int64_t S, int64_t E) {
-    return 4 * ((E + 2) + 1 + S + 2 * gather_grouped_max_tiles(S, E));
+    return 4 * ((E + 2) + 1 + S + 2 * gather_grouped_max_tiles(S, E, kGatherGemvRows));
 }
 
-int64_t gather_grouped_max_tiles(int64_t S, int64_t E) { return S / kBM + E + 1; }
+GatherPlan gather_plan_layout(void* workspace, int64_t S, int64_t E, int tr) {
+    GatherPlan p;
+    p.seg = static_cast<int32_t*>(workspace);
+    p.ntiles = p.seg + E + 2;
+    p.perm = p.ntiles + 1;
+    p.tiles = p.perm + S;
+    p.max_tiles = gather_grouped_max_tiles(S, E, tr);
+    return p;
+}
+
+hipError_t launch_gather_plan(const int32_t* idx, int64_t S, int64_t E, int tr, const GatherPlan& p,
+                              hipStream_t stream) {
+    const size_t plan_lds = 2 * (size_t)(E + 1) * sizeof(int32_t);
+    hipLaunchKernelGGL(gather_plan_kernel, dim3(1), dim3(1024), plan_lds, stream, idx, (int)S, (int)E, tr, p.seg,
+                       p.ntiles, p.perm, p.tiles);
+    return hipGetLastError();
+}
 
 hipError_t launch_gather_grouped(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_index,
                                  int64_t experts, int64_t x_bytes, void* workspace) {
     const int64_t S = T * top_k;
-    int32_t* ws = static_cast<int32_t*>(workspace);
-    int32_t* seg = ws;
-    int32_t* ntiles = seg + experts + 2;
-    int32_t* perm = ntiles + 1;
-    int32_t* tiles = perm + S;
-    const int64_t mt = gather_grouped_max_tiles(S, experts);
-    const size_t plan_lds = 2 * (size_t)(experts + 1) * sizeof(int32_t);
-    hipLaunchKernelGGL(gather_plan_kernel, dim3(1), dim3(1024), plan_lds, a.stream, idx, (int)S, (int)experts, seg,
-                       ntiles, perm, tiles);
-    hipError_t e = hipGetLastError();
+    const GatherPlan pl = gather_plan_layout(workspace, S, experts, kBM);
+    hipError_t e = launch_gather_plan(idx, S, experts, kBM, pl, a.stream);
     if (e != hipSuccess) return e;
+    const int64_t mt = pl.max_tiles;
+    int32_t *perm = pl.perm, *seg = pl.seg, *tiles = pl.tiles, *ntiles = pl.ntiles;
     const QmmGather gq{perm, seg, tiles, ntiles, top_k, x_per_index, (int)experts, (uint32_t)x_bytes};
     if (a.bits == 4)
         return a.sb_dtype == DT_F16 ? launch_gather_bn<4, DT_F16>(a, gq, mt) : launch_gather_bn<4, DT_BF16>(a, gq, mt);

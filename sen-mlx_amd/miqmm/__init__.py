@@ -225,7 +225,10 @@ def quantized_matmul_grouped(xs, ws, scales, biases, group_size: int = 64, bits:
     return outs
 
 
-GROUPED_MIN_PER_EXPERT = 8  # selections per expert from which the grouped path is used (api.cpp)
+# selections per expert (on average) from which gather_qmm groups them by
+# expert (api.cpp): on the tiled MFMA matmul from 8, on the MFMA GEMV from 4
+GROUPED_MIN_PER_EXPERT = 8
+GROUPED_GEMV_MIN_PER_EXPERT = 4
 
 
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
@@ -286,7 +289,7 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
     elif out.shape != shape or not out.is_contiguous() or out.dtype != ydt:
         raise MiqmmError(EINVAL, f"out must be contiguous {shape} of {ydt}")
     ws, ws_bytes = None, 0
-    if grouped is not False and M == 1 and batch * top_k >= GROUPED_MIN_PER_EXPERT * E:
+    if grouped is not False and M == 1 and batch * top_k >= GROUPED_GEMV_MIN_PER_EXPERT * E:
         nb = ctypes.c_int64()
         _check(lib().miqmm_gather_qmm_workspace_size(batch, top_k, E, ctypes.byref(nb)))
         ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=x.device)

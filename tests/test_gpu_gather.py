@@ -121,8 +121,10 @@ def test_gather_deepseek_decode_shapes_equal_quantized_matmul(gpu, c_oracle, bit
         idx = torch.stack([torch.randperm(E, generator=gen)[:top_k] for _ in range(T)]).to(torch.int32).cuda()
         x = m.synth_problem(T, 8, H, g, bits, seed=3, stream_id=T)[0].reshape(T, 1, 1, H)
         h = m.synth_problem(T * top_k, 8, I, g, bits, seed=4, stream_id=T)[0].reshape(T, top_k, 1, I)
-        yg = m.gather_qmm(x, gw, gs, gb, idx, True, g, bits)
-        yd = m.gather_qmm(h, dw, ds, db, idx, True, g, bits)
+        # the per-selection path (the 64-token batch would otherwise be grouped
+        # by expert, whose MFMA GEMV sums in another order)
+        yg = m.gather_qmm(x, gw, gs, gb, idx, True, g, bits, grouped=False)
+        yd = m.gather_qmm(h, dw, ds, db, idx, True, g, bits, grouped=False)
         assert yg.shape == (T, top_k, 1, I) and yd.shape == (T, top_k, 1, H)
         torch.cuda.synchronize()
         idx_h = idx.cpu().numpy()
@@ -214,6 +216,46 @@ def test_gather_grouped_matches_oracle(gpu, c_oracle, bits, g, sbd, E, N, K, T, 
     yf = y.float().cpu().numpy()
     for t, j in bad:
         assert not yf[t, j].any()
+
+
+# (bits, g, scale dtype, E, N, K, tokens, top_k, x shared, skew) -- 4 to 8
+# selections per expert: the expert-grouped MFMA GEMV (16 selections per
+# tile); skew sends most selections to expert 0, which then spans tiles
+GROUPED_GEMV = [
+    (4, 64, O.BF16, 16, 200, 512, 40, 2, True, False),
+    (8, 32, O.F16, 8, 136, 384, 12, 3, False, False),
+    (4, 128, O.BF16, 4, 320, 1024, 12, 2, True, False),
+    (4, 64, O.F16, 8, 96, 256, 40, 1, True, True),
+    (8, 64, O.BF16, 8, 64, 512, 20, 2, False, True),
+]
+
+
+@pytest.mark.parametrize("bits,g,sbd,E,N,K,T,top_k,shared,skew", GROUPED_GEMV)
+def test_gather_grouped_gemv_matches_oracle(gpu, c_oracle, bits, g, sbd, E, N, K, T, top_k, shared, skew):
+    """the expert-grouped MFMA GEMV (selections grouped by expert on the
+    device, each selected expert's weights streamed once for up to 16 of its
+    selections, exact fp32 dequant) against the oracle, with out-of-range ids;
+    and against the per-selection path"""
+    m = _miqmm()
+    (w, s, b), (wd, sd, bd) = _experts(E, N, K, g, bits, sbd, seed=E * 11 + K)
+    rng = np.random.default_rng(N + T + 1)
+    idx = rng.integers(0, E, size=(T, top_k)).astype(np.int32)
+    if skew:
+        idx[: (3 * T) // 4, 0] = 0
+    idx[rng.integers(0, T, size=2), -1] = -3  # out of range: zero rows
+    xshape = (T, 1, 1) if shared else (T, top_k, 1)
+    x, xd = _x(xshape, K, seed=T + 7)
+    ti = torch.from_numpy(idx).cuda()
+    y = m.gather_qmm(xd, wd, sd, bd, ti, True, g, bits, grouped=True)
+    assert y.shape == (T, top_k, 1, N)
+    ref = O.gather_qmm_f64(x, w, s, b, idx, K, g, bits, sb_dtype=sbd)
+    check(y, ref, True, f"grouped GEMV bits={bits} g={g} E={E} N={N} K={K} T={T} k={top_k} shared={shared}")
+    yf = y.float().cpu().numpy()
+    for t, j in np.argwhere((idx < 0) | (idx >= E)):
+        assert not yf[t, j].any()
+    ys = m.gather_qmm(xd, wd, sd, bd, ti, True, g, bits, grouped=False)
+    rep = O.parity_report(yf.astype(np.float64), ys.float().cpu().numpy().astype(np.float64))
+    assert rep["max_err"] <= rep["mag_bar"] and rep["max_err"] <= rep["ulp2_bar"], rep
 
 
 def test_gather_grouped_deepseek_prefill(gpu, c_oracle):
