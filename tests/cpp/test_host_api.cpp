@@ -118,7 +118,8 @@ static void test_gather() {
     };
     const Case cases[] = {{"gather_qmm shared x [3,1,1,K] x idx [3,2] (+ out-of-range id)", 3, 2, false, false},
                           {"gather_qmm per-selection x [3,2,1,K]", 3, 2, true, false},
-                          {"SwitchLinear grouped x [96,1,1,K] x idx [96,2] with workspace", 96, 2, false, true}};
+                          {"SwitchLinear grouped x [96,1,1,K] x idx [96,2] with workspace", 96, 2, false, true},
+                          {"SwitchLinear grouped GEMV x [10,2,1,K] x idx [10,2] with workspace", 10, 2, true, true}};
     for (const Case& c : cases) {
         const int64_t S = c.batch * c.top_k, xm = c.per_index ? S : c.batch;
         Dev<uint16_t> x(xm * K), y(S * N);

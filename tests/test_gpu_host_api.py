@@ -22,5 +22,5 @@ def test_cpp_host_api(gpu, tmp_path):
     print(r.stdout)
     assert r.returncode == 0 and "PASSED" in r.stdout, r.stdout + r.stderr
     for name in ("embed_tokens: QuantizedEmbedding", "q_proj: QuantizedLinear", "down_proj: QuantizedLinear",
-                 "gate_proj: SwitchLinear", "SwitchLinear grouped"):
+                 "gate_proj: SwitchLinear", "SwitchLinear grouped x", "SwitchLinear grouped GEMV"):
         assert any(line.startswith("ok") and name in line for line in r.stdout.splitlines()), name
