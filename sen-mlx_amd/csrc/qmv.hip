@@ -33,7 +33,12 @@
 namespace miqmm {
 namespace {
 
-constexpr int kMaxBlocksPerCU = 8;
+// blocks per CU at most, beyond which the waves walk several tiles each:
+// 4 for the matrix GEMVs (measured on MI355X: N = 14336, K = 4096, M = 1 at
+// R = 2, 10.2 us with a cap of 8, 9.8 with 4), 8 for the expert gather (its
+// per-selection tiles: 16 tokens of DeepSeek-V2-Lite 39.5 us at 8, 42.5 at 4)
+constexpr int kMaxBlocksPerCU = 4;
+constexpr int kMaxGatherBlocksPerCU = 8;
 constexpr int kNumCUs = 256;
 constexpr int64_t kFillTiles = 1536;  // row tiles that keep the chip busy (see pick_r)
 
@@ -401,10 +406,10 @@ int use_ksplit(int64_t tiles, int64_t K, int bits, int L) {
 }
 
 // blocks of 4 waves: one tile per wave (or per block when split), at most
-// kMaxBlocksPerCU blocks per CU, the waves then walking further tiles
-int gemv_blocks(int64_t tiles, int ksplit) {
+// per_cu blocks per CU, the waves then walking further tiles
+int gemv_blocks(int64_t tiles, int ksplit, int per_cu = kMaxBlocksPerCU) {
     const int64_t want = ksplit ? tiles : (tiles + 3) / 4;
-    return (int)(want < kNumCUs * kMaxBlocksPerCU ? want : kNumCUs * kMaxBlocksPerCU);
+    return (int)(want < (int64_t)kNumCUs * per_cu ? want : (int64_t)kNumCUs * per_cu);
 }
 
 // a[0..count) share M, K, group size, bits and dtypes; one grid covers all
@@ -470,7 +475,7 @@ hipError_t launch_gather_t(const QmmArgs& a, const int32_t* idx, int64_t T, int 
     if (tiles >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
     P.tiles = (int)tiles;
     P.ksplit = use_ksplit(tiles, a.K, a.bits, L);
-    const int blocks = gemv_blocks(tiles, P.ksplit);
+    const int blocks = gemv_blocks(tiles, P.ksplit, kMaxGatherBlocksPerCU);
     const int gs_shift = __builtin_ctz((unsigned)a.group_size);
     hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 2>), dim3(blocks), dim3(256), 0, a.stream, P, (int)a.M,
                        (int)a.K, gs_shift, a.y_dtype);
@@ -501,9 +506,11 @@ int pick_l(int64_t K, int bits) {
 // small N then leaves most of the chip idle and the launch latency-bound: take
 // the largest R that still gives kFillTiles row tiles, else 1 (measured on
 // MI355X, 4-bit g64, M = 1: N = 896 runs 2.60 -> 2.16 us with R = 1, N = 9728
-// 4.12 -> 3.80 us with R = 2, N = 14336 at K = 4096 is best at R = 4).
-int pick_r(int64_t M, int64_t rows, int L) {
-    const int rmax = M <= 2 ? 4 : M <= 4 ? 2 : 1;
+// 4.12 -> 3.80 us with R = 2).  One row of x with rows of at least
+// kMinXTableK codes (read from the LDS x table, so more rows no longer save
+// x loads): at most 2 (N = 14336 at K = 4096: 10.4 -> 9.9 us against R = 4).
+int pick_r(int64_t M, int64_t rows, int L, int64_t K) {
+    const int rmax = M <= 1 && K >= kMinXTableK ? 2 : M <= 2 ? 4 : M <= 4 ? 2 : 1;
     const int64_t sg = 64 / L;
     for (int r = rmax; r > 1; r /= 2)
         if ((rows + sg * r - 1) / (sg * r) >= kFillTiles) return r;
@@ -536,7 +543,7 @@ template <int BITS, int SBT>
 hipError_t launch_mt(const QmmArgs* a, int count) {
     int64_t rows = 0;
     for (int i = 0; i < count; ++i) rows += a[i].N;
-    const int r = pick_r(a[0].M, rows, pick_l(a[0].K, a[0].bits));
+    const int r = pick_r(a[0].M, rows, pick_l(a[0].K, a[0].bits), a[0].K);
     switch (pick_mt(a[0].M)) {
         case 1: return launch_r<BITS, SBT, 1>(a, count, r);
         case 2: return launch_r<BITS, SBT, 2>(a, count, r);
@@ -550,12 +557,12 @@ hipError_t launch_mt(const QmmArgs* a, int count) {
 
 bool qmv_ksplit(int64_t M, int64_t N, int64_t K, int bits) {
     const int L = pick_l(K, bits);
-    const int64_t tile = (64 / L) * pick_r(M, N, L);
+    const int64_t tile = (64 / L) * pick_r(M, N, L, K);
     return use_ksplit((N + tile - 1) / tile, K, bits, L) != 0;
 }
 
 void qmv_config(const QmmArgs& a, int* rows_per_subgroup, int* m_tile, int* lanes_per_row) {
-    if (rows_per_subgroup) *rows_per_subgroup = pick_r(a.M, a.N, pick_l(a.K, a.bits));
+    if (rows_per_subgroup) *rows_per_subgroup = pick_r(a.M, a.N, pick_l(a.K, a.bits), a.K);
     if (m_tile) *m_tile = pick_mt(a.M);
     if (lanes_per_row) *lanes_per_row = pick_l(a.K, a.bits);
 }
@@ -582,7 +589,7 @@ hipError_t gather_l(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, 
 template <int BITS, int SBT>
 hipError_t gather_mt(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int xpe, int64_t E, int64_t xs,
                      int64_t ys) {
-    const int r = pick_r(a.M, a.N * T * top_k, pick_l(a.K, a.bits));
+    const int r = pick_r(a.M, a.N * T * top_k, pick_l(a.K, a.bits), 0);  // gather: no x table
     switch (pick_mt(a.M)) {
         case 1:
             return r == 4   ? gather_l<BITS, SBT, 1, 4>(a, idx, T, top_k, xpe, E, xs, ys)
