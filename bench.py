@@ -128,26 +128,28 @@ def time_graphs(torch, graphs, reps):
     return start.elapsed_time(end) / 1e3
 
 
-def kernel_roofline(miqmm, torch, N, K, M, replicas, launches_per_graph, reps):
+def kernel_roofline(miqmm, torch, N, K, M, replicas, launches_per_graph, reps, g=64, bits=4, sb_dtype=None):
     """average duration of back-to-back launches of one shape over rotating
     weight replicas (cold in the Infinity Cache); returns (avg_s, bytes_per_launch)"""
+    sb_dtype = sb_dtype or torch.bfloat16
+    ydt = miqmm.result_type(torch.bfloat16, sb_dtype)
     sets = []
     for r in range(replicas):
-        x, w, s, b = miqmm.synth_problem(M, N, K, 64, 4, seed=100 + r, stream_id=N + K)
-        sets.append((x, w, s, b, torch.empty((M, N), dtype=torch.bfloat16, device="cuda")))
+        x, w, s, b = miqmm.synth_problem(M, N, K, g, bits, sb_dtype=sb_dtype, seed=100 + r, stream_id=N + K)
+        sets.append((x, w, s, b, torch.empty((M, N), dtype=ydt, device="cuda")))
 
     def body():
         for i in range(launches_per_graph):
             x, w, s, b, y = sets[i % replicas]
-            miqmm.quantized_matmul(x, w, s, b, True, 64, 4, out=y)
+            miqmm.quantized_matmul(x, w, s, b, True, g, bits, out=y)
 
     body()
     torch.cuda.synchronize()
-    g = capture(torch, body)
-    g.replay()
-    t = time_graphs(torch, [g], reps)
+    graph = capture(torch, body)
+    graph.replay()
+    t = time_graphs(torch, [graph], reps)
     del sets
-    return t / (reps * launches_per_graph), qbytes(M, N, K)
+    return t / (reps * launches_per_graph), qbytes(M, N, K, bits, g, yb=4 if ydt == torch.float32 else 2)
 
 
 def qmm_tflops(miqmm, torch, M, N, K, iters):
@@ -233,6 +235,29 @@ def graph_avg(torch, fns, launches, reps):
     torch.cuda.synchronize()
     t = time_graphs(torch, [g], reps)
     return t / (reps * launches)
+
+
+def small_m_and_large_vocab(miqmm, torch):
+    """the GEMV routes beyond the decode step: speculative-verify / small-batch
+    rows M in {1, 2, 4, 8, 16} on the Llama-3-8B projections (4-bit g64), and
+    the Gemma-3-27B-class head K = 5376, N = 262144 at M in {1, 8} with fp16
+    scales, 4-bit g32 and 8-bit g64; weights cold (rotating replicas)"""
+    res = {}
+    for (N, K) in [(6144, 4096), (4096, 4096), (14336, 4096), (4096, 14336)]:
+        for M in (1, 2, 4, 8, 16):
+            avg, nb = kernel_roofline(miqmm, torch, N, K, M, replicas=10, launches_per_graph=40, reps=3)
+            res[f"qmv_m{M}_{K}to{N}"] = {"us": round(avg * 1e6, 2), "GB/s": round(nb / avg / 1e9, 1),
+                                         "frac_hbm": round(nb / avg / 1e9 / HBM_PEAK_GBS, 4)}
+        torch.cuda.empty_cache()
+    for (bits, g) in [(4, 32), (8, 64)]:
+        for M in (1, 8):
+            avg, nb = kernel_roofline(miqmm, torch, 262144, 5376, M, replicas=2, launches_per_graph=8, reps=3,
+                                      g=g, bits=bits, sb_dtype=torch.float16)
+            res[f"head_5376to262144_m{M}_{bits}bit_g{g}_f16"] = {
+                "us": round(avg * 1e6, 2), "GB/s": round(nb / avg / 1e9, 1),
+                "frac_hbm": round(nb / avg / 1e9 / HBM_PEAK_GBS, 4)}
+        torch.cuda.empty_cache()
+    return res
 
 
 def moe_and_embedding(miqmm, torch):
@@ -420,6 +445,9 @@ def main():
         head["dense_bf16_gemm_m2048_4096to14336_torch"] = {
             "TFLOP/s": round(dense_bf16_tflops(torch, 2048, 14336, 4096, 10), 1)}
         out["headline"] = head
+        torch.cuda.empty_cache()
+        out["small_m_and_large_vocab"] = small_m_and_large_vocab(miqmm, torch)
+        print(f"# small M / large vocab: {json.dumps(out['small_m_and_large_vocab'])}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
         out["moe_and_embedding"] = moe_and_embedding(miqmm, torch)
         print(f"# moe/embedding: {json.dumps(out['moe_and_embedding'])}", file=sys.stderr, flush=True)

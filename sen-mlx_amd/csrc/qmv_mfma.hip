@@ -310,18 +310,21 @@ hipError_t launch_t(const QmmArgs& a) {
 
 int pick_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
-// tiles per block and waves per block: T=4 amortises the x operand over four
-// 16-row tiles; two tiles when four would leave too few waves in flight, when
-// the cross-wave reduction would need more than 32 KiB of LDS, or (8-bit) when
-// 16 waves per block leave too few registers for four tiles; 16 K-splitting
-// waves once K has at least 16 k-quads, else 4
+// tiles per block and waves per block: 16 K-splitting waves once K has at
+// least 64 k-quads (K >= 8192), else 4; then the most 16-row tiles per block
+// (4, 2 or 1: more tiles amortise the x operand) that still give a block per
+// CU.  Measured on MI355X (4-bit g64, M = 8 / 16): 4096 -> 14336 30.2 / 40.6
+// -> 26.8 / 32.0 us, 14336 -> 4096 45.3 / 53.3 -> 29.6 / 37.0 us, 4096 ->
+// 4096 17.7 / 20.8 -> 12.0 / 15.5 us against the earlier choice (16 waves from
+// K = 2048, four tiles unless too few waves in flight).
 void pick_tw(int64_t M, int64_t N, int64_t K, int bits, int* T, int* WPB) {
     const int64_t KQ = (K / 32 + 3) / 4;
     const int nmt = M > 4 ? (M > 8 ? 4 : 2) : 1;
-    const int wpb = KQ >= 16 ? 16 : 4;
+    const int wpb = KQ >= 64 ? 16 : 4;
     int t = 4;
-    if (((N + 63) / 64) * wpb < 2048 || wpb * 4 * 64 * nmt * 4 > 32768) t = 2;
-    if (bits == 8 && wpb == 16) t = 2;  // 8-bit stages need the registers of two tiles
+    while (t > 1 && (N + 16 * t - 1) / (16 * t) < 256) t /= 2;
+    while (t > 1 && wpb * t * 64 * nmt * 4 > 32768) t /= 2;  // cross-wave reduction LDS
+    if (bits == 8 && wpb == 16 && t > 2) t = 2;  // 8-bit stages need the registers of two tiles
     *T = t;
     *WPB = wpb;
 }
@@ -335,6 +338,7 @@ template <int BITS, int SBT, int MT>
 hipError_t launch_tt(const QmmArgs& a) {
     int T, WPB;
     pick_tw(a.M, a.N, a.K, a.bits, &T, &WPB);
+    if (T == 1) return launch_w<BITS, SBT, MT, 1>(a, WPB);
     return T == 4 ? launch_w<BITS, SBT, MT, 4>(a, WPB) : launch_w<BITS, SBT, MT, 2>(a, WPB);
 }
 

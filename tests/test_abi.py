@@ -190,7 +190,7 @@ def test_query_route(lib):
     assert miqmm.query_route(2, 128, 96, 32, 4)[0] == miqmm.ROUTE_QMV_DOT
     for M in (5, 8, 16):
         route, tiles = miqmm.query_route(M, 14336, 4096, 64, 4)
-        assert route == miqmm.ROUTE_QMV and tiles[0] in (2, 4) and tiles[1] >= M and tiles[2] in (4, 16)
+        assert route == miqmm.ROUTE_QMV and tiles[0] in (1, 2, 4) and tiles[1] >= M and tiles[2] in (4, 16)
     route, tiles = miqmm.query_route(2048, 14336, 4096, 64, 4)
     assert route == miqmm.ROUTE_QMM and tiles[2] == 64
     with pytest.raises(miqmm.MiqmmError) as e:
