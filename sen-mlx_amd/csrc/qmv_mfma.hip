@@ -188,17 +188,25 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
     };
 
     // apply the dequant of one group cycle c (groups c*GS .. c*GS+GS-1) and clear D
+    // This lane's four D rows r = 4q + j hold groups c*GS + r % GS: with
+    // GS < 4 only GS of them differ (r % GS = j % GS), so each distinct
+    // scale / bias is loaded once (M = 16: one pair per row instead of four)
+    constexpr int NG = GS < 4 ? GS : 4;
     auto rescale = [&](int c) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const uint32_t row = (uint32_t)(16 * t + nl);
+            float sv[NG], bv[NG];
+#pragma unroll
+            for (int jj = 0; jj < NG; ++jj) {
+                const int g = c * GS + ((4 * q + jj) % GS);
+                const uint32_t off = g < G ? (row * G + g) * 2 : kOOB;
+                sv[jj] = half_to_f32<SBT>(bload2(sr, off));
+                bv[jj] = half_to_f32<SBT>(bload2(br, off)) - kCentre * sv[jj];
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int r = 4 * q + j;
-                const int g = c * GS + (r % GS);
-                const uint32_t off = g < G ? (row * G + g) * 2 : kOOB;
-                const float s = half_to_f32<SBT>(bload2(sr, off));
-                const float b = half_to_f32<SBT>(bload2(br, off)) - kCentre * s;
+                const float s = sv[GS >= 4 ? j : j % GS], b = bv[GS >= 4 ? j : j % GS];
                 const int mi = GS >= 4 ? 0 : j / GS;  // which of this lane's m (compile time)
                 tot[t][mi] = fmaf(s, D[t][j], tot[t][mi]);
                 tot[t][mi] = fmaf(b, DX[j], tot[t][mi]);
