@@ -193,6 +193,15 @@ def test_query_route(lib):
         assert route == miqmm.ROUTE_QMV and tiles[0] in (1, 2, 4) and tiles[1] >= M and tiles[2] in (4, 16)
     route, tiles = miqmm.query_route(2048, 14336, 4096, 64, 4)
     assert route == miqmm.ROUTE_QMM and tiles[2] == 64
+    # the qmm plan (rounds of one tile per CU): width and k ranges
+    for (M, N, K), (bn, ks) in {(2048, 14336, 4096): (256, 1), (2048, 6144, 4096): (256, 1),
+                                (2048, 4096, 4096): (128, 1), (2048, 4096, 14336): (256, 2),
+                                (256, 4096, 4096): (128, 4), (32, 64, 256): (128, 1)}.items():
+        route, tiles = miqmm.query_route(M, N, K, 64, 4)
+        assert route == miqmm.ROUTE_QMM and tiles == (256, bn, 64, ks), ((M, N, K), tiles)
+    # the MFMA GEMV's launch shape: one block per CU at the most tiles per block
+    assert miqmm.query_route(8, 14336, 4096, 64, 4)[1] == (2, 8, 4, 0)
+    assert miqmm.query_route(16, 4096, 14336, 64, 4)[1] == (1, 16, 16, 0)
     with pytest.raises(miqmm.MiqmmError) as e:
         miqmm.query_route(1, 64, 96, 64, 4)
     assert e.value.status == miqmm.EINVAL
