@@ -34,6 +34,7 @@
 // Rounding the dequantized weight to bf16 before the MFMA follows MLX's qmm,
 // which dequantizes W tiles into threadgroup memory in the activation type.
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "miqmm_device.h"
@@ -576,12 +577,16 @@ template <int BITS, int SBT, int BN, bool GATHER>
 hipError_t launch_t(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles, const QmmSplit& sp) {
     constexpr size_t lds = qmm_lds_bytes<BITS, BN>();
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
-    static bool attr_set = false;  // the attribute is per kernel; setting it twice is harmless
-    if (!attr_set) {
+    // the LDS attribute, once per device (a bit per device id; two threads
+    // racing both set it, which is harmless)
+    static std::atomic<uint64_t> attr_set{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev >= 64) return hipErrorInvalidDevice;
+    if (!(attr_set.load(std::memory_order_relaxed) >> dev & 1)) {
         hipError_t e = hipFuncSetAttribute((const void*)qmm_kernel<BITS, SBT, BN, GATHER>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        attr_set = true;
+        attr_set.fetch_or(uint64_t{1} << dev, std::memory_order_relaxed);
     }
     const dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)m_tiles, (unsigned)sp.ks);
     const int gs_shift = __builtin_ctz((unsigned)a.group_size);

@@ -34,6 +34,8 @@
 //
 // Work: a block is 4 waves = (4 / KS) row tiles of 16 x KS contiguous
 // k-ranges; the KS partial sums of a tile are combined through LDS.
+#include <atomic>
+
 #include "miqmm_device.h"
 #include "miqmm_internal.h"
 
@@ -381,12 +383,16 @@ hipError_t launch_t(const QmmArgs& a, int KS) {
     using S = Shape<BITS, GSH, MT>;
     const int G = (int)(a.K >> GSH);
     const Lds L = lds_layout(MT, (int)a.K, G, S::STAGE_BYTES);
-    static bool attr_set = false;  // the attribute is per kernel; setting it twice is harmless
-    if (!attr_set) {
+    // the LDS attribute, once per device (a bit per device id; two threads
+    // racing both set it, which is harmless)
+    static std::atomic<uint64_t> attr_set{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev >= 64) return hipErrorInvalidDevice;
+    if (!(attr_set.load(std::memory_order_relaxed) >> dev & 1)) {
         hipError_t e = hipFuncSetAttribute((const void*)qmvx_kernel<BITS, SBT, MT, GSH>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
-        attr_set = true;
+        attr_set.fetch_or(uint64_t{1} << dev, std::memory_order_relaxed);
     }
     const int64_t tiles = (a.N + 15) / 16;
     int blocks;
