@@ -508,9 +508,12 @@ int pick_l(int64_t K, int bits) {
 // MI355X, 4-bit g64, M = 1: N = 896 runs 2.60 -> 2.16 us with R = 1, N = 9728
 // 4.12 -> 3.80 us with R = 2).  One row of x with rows of at least
 // kMinXTableK codes (read from the LDS x table, so more rows no longer save
-// x loads): at most 2 (N = 14336 at K = 4096: 10.4 -> 9.9 us against R = 4).
+// x loads): at most 2 (N = 14336 at K = 4096: 10.4 -> 9.9 us against R = 4),
+// except for rows of 8192 codes or more, where four rows keep more of W in
+// flight per wave (N = 8192 at K = 28672: 37.4 -> 31.3 us, N = 28672 at
+// K = 8192: 31.7 -> 30.0 us; R = 1 there: 45.7 and 37.3 us).
 int pick_r(int64_t M, int64_t rows, int L, int64_t K) {
-    const int rmax = M <= 1 && K >= kMinXTableK ? 2 : M <= 2 ? 4 : M <= 4 ? 2 : 1;
+    const int rmax = M <= 1 && K >= kMinXTableK ? (K >= 8192 ? 4 : 2) : M <= 2 ? 4 : M <= 4 ? 2 : 1;
     const int64_t sg = 64 / L;
     for (int r = rmax; r > 1; r /= 2)
         if ((rows + sg * r - 1) / (sg * r) >= kFillTiles) return r;

@@ -180,6 +180,11 @@ def test_query_route(lib):
     route, tiles = miqmm.query_route(1, 14336, 4096, 64, 4)
     assert route == miqmm.ROUTE_QMV_DOT and tiles[0] in (1, 2, 4) and tiles[1] >= 1 and tiles[2] in (16, 32, 64)
     assert miqmm.query_route(1, 4864, 896, 64, 4)[1][2] == 32  # 28 chunks per row -> 32 lanes
+    # rows per sub-group at M = 1: two from the x table on, four for rows of
+    # 8192 codes or more while four still give 1536 row tiles
+    assert miqmm.query_route(1, 14336, 4096, 64, 4)[1][0] == 2
+    assert miqmm.query_route(1, 8192, 28672, 64, 4)[1][0] == 4
+    assert miqmm.query_route(1, 4096, 14336, 64, 4)[1][0] == 2
     # wide, short-K head at M = 1 and 2 <= M <= 4: the LDS-staged MFMA GEMV (m tile, k-splits, codes per stage)
     route, tiles = miqmm.query_route(1, 151936, 896, 64, 4)
     assert route == miqmm.ROUTE_QMVX and tiles[:3] == (1, 1, 1024)
