@@ -320,17 +320,21 @@ int pick_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 
 
 // tiles per block and waves per block: 16 K-splitting waves once K has at
 // least 64 k-quads (K >= 8192), else 4; then the most 16-row tiles per block
-// (4, 2 or 1: more tiles amortise the x operand) that still give a block per
-// CU.  Measured on MI355X (4-bit g64, M = 8 / 16): 4096 -> 14336 30.2 / 40.6
+// (4, 2 or 1: more tiles amortise the x operand, which every block reads
+// whole from L2) that still give 192 blocks, three quarters of the CUs.
+// Measured on MI355X (4-bit g64, M = 8 / 16): 4096 -> 14336 30.2 / 40.6
 // -> 26.8 / 32.0 us, 14336 -> 4096 45.3 / 53.3 -> 29.6 / 37.0 us, 4096 ->
 // 4096 17.7 / 20.8 -> 12.0 / 15.5 us against the earlier choice (16 waves from
-// K = 2048, four tiles unless too few waves in flight).
+// K = 2048, four tiles unless too few waves in flight); then 192 blocks
+// instead of 256: 4096 -> 14336 at M = 8 26.3 -> 25.2 us, 4096 -> 6144
+// 16.2 / 21.3 -> 15.7 / 19.7 us, the rest unchanged (128 blocks: 4096 ->
+// 4096 at M = 16 15.5 -> 19.4 us).
 void pick_tw(int64_t M, int64_t N, int64_t K, int bits, int* T, int* WPB) {
     const int64_t KQ = (K / 32 + 3) / 4;
     const int nmt = M > 4 ? (M > 8 ? 4 : 2) : 1;
     const int wpb = KQ >= 64 ? 16 : 4;
     int t = 4;
-    while (t > 1 && (N + 16 * t - 1) / (16 * t) < 256) t /= 2;
+    while (t > 1 && (N + 16 * t - 1) / (16 * t) < 192) t /= 2;
     while (t > 1 && wpb * t * 64 * nmt * 4 > 32768) t /= 2;  // cross-wave reduction LDS
     if (bits == 8 && wpb == 16 && t > 2) t = 2;  // 8-bit stages need the registers of two tiles
     *T = t;

@@ -204,8 +204,8 @@ def test_query_route(lib):
                                 (256, 4096, 4096): (128, 4), (32, 64, 256): (128, 1)}.items():
         route, tiles = miqmm.query_route(M, N, K, 64, 4)
         assert route == miqmm.ROUTE_QMM and tiles == (256, bn, 64, ks), ((M, N, K), tiles)
-    # the MFMA GEMV's launch shape: one block per CU at the most tiles per block
-    assert miqmm.query_route(8, 14336, 4096, 64, 4)[1] == (2, 8, 4, 0)
+    # the MFMA GEMV's launch shape: the most tiles per block that still give 192 blocks
+    assert miqmm.query_route(8, 14336, 4096, 64, 4)[1] == (4, 8, 4, 0)  # 224 blocks of four tiles
     assert miqmm.query_route(16, 4096, 14336, 64, 4)[1] == (1, 16, 16, 0)
     with pytest.raises(miqmm.MiqmmError) as e:
         miqmm.query_route(1, 64, 96, 64, 4)
