@@ -22,9 +22,10 @@
  *   y       [M, N]            dtype y_dtype (bf16, fp16 or fp32)
  *   y[m,n] = sum_k x[m,k] * (scales[n,k/g] * q[n,k] + biases[n,k/g])
  *
- * All pointers are device pointers owned by the caller; nothing is allocated
- * on the matmul path.  Calls are asynchronous on `stream` (a hipStream_t;
- * NULL = the default stream).  Every function returns a miqmm_status; on
+ * All pointers are device pointers owned by the caller; no entry point
+ * allocates device memory, synchronizes or waits on the host.  Calls are
+ * asynchronous on `stream` (a hipStream_t; NULL = the default stream) and may
+ * be captured into a HIP graph.  Every function returns a miqmm_status; on
  * failure miqmm_last_error() returns a message for the calling thread.
  * Calls are safe from several threads on distinct streams.
  */
@@ -49,13 +50,16 @@ typedef enum { MIQMM_DT_BF16 = 0, MIQMM_DT_F16 = 1, MIQMM_DT_F32 = 2 } miqmm_dty
 /* QMV: small-M GEMV on MFMA with exact integer codes; QMM: large-M tiled MFMA
  * with bf16-dequantized W tiles; QMV_DOT: small-M GEMV on v_dot2 (no MFMA);
  * QMVX: small-M GEMV on MFMA with x staged in LDS (M <= 4 per pass, needs
- * K/group_size even and min(M,4)*K <= 32768). */
+ * K/group_size even and min(M,4)*K <= 32768); QMVS: one-row GEMV on v_dot2
+ * with K cut into 1 KiB slices of codes, one wave per slice (M == 1, needs
+ * K*bits/8 <= 15 KiB, K/group_size even, scales and biases 4-byte aligned). */
 typedef enum {
     MIQMM_ROUTE_AUTO = 0,
     MIQMM_ROUTE_QMV = 1,
     MIQMM_ROUTE_QMM = 2,
     MIQMM_ROUTE_QMV_DOT = 3,
-    MIQMM_ROUTE_QMVX = 4
+    MIQMM_ROUTE_QMVX = 4,
+    MIQMM_ROUTE_QMVS = 5
 } miqmm_route;
 
 /*
@@ -64,9 +68,11 @@ typedef enum {
  * (reached at src/engine/mlx_lm/utils/mod.rs:70-78 and from every
  * QuantizedLinear::forward).  transpose must be 1; bits in {4, 8};
  * group_size in {32, 64, 128}; K % group_size == 0; x and w 16-byte aligned.
- * M == 0 is a no-op.  Route (HBM-bound GEMVs for M <= 16): M == 1 -> qmv_dot,
- * or qmvx for N >= 65536 with K <= 2048; 2 <= M <= 4 -> qmvx where supported,
- * else qmv_dot; M <= 16 -> qmv; else qmm (MFMA-bound tiled matmul).
+ * M == 0 is a no-op.  Route (HBM-bound GEMVs for M <= 16): M == 1 -> qmvs
+ * for K >= 2048 (with K*bits/8 <= 15 KiB, K/group_size even and 4-byte
+ * aligned scales and biases), else qmv_dot, or qmvx for
+ * N >= 65536 with K <= 2048; 2 <= M <= 4 -> qmvx where supported, else
+ * qmv_dot; M <= 16 -> qmv; else qmm (MFMA-bound tiled matmul).
  */
 int miqmm_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
                            const void* biases, int64_t M, int64_t N, int64_t K, int transpose,
@@ -113,6 +119,36 @@ int miqmm_quantized_matmul_ex(void* y, const void* x, const uint32_t* w, const v
                               const void* biases, int64_t M, int64_t N, int64_t K, int transpose,
                               int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
                               int route, void* stream);
+
+/*
+ * Bytes of scratch that miqmm_quantized_matmul_ws would use for this shape
+ * (the fp32 partials of the tiled matmul's k split: k ranges * M * N * 4
+ * when the plan splits the k-steps over several blocks per output tile,
+ * which pays when the output tiles are fewer than the CUs, else 0).
+ * No reference counterpart: the workspace query of the caller that can
+ * pass scratch memory.
+ */
+int miqmm_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                                          int64_t* bytes);
+
+/*
+ * miqmm_quantized_matmul (+ bias when non-null, as miqmm_quantized_linear)
+ * with a caller-owned device workspace (16-byte aligned, any contents;
+ * NULL / 0 bytes: no split).  With at least
+ * miqmm_quantized_matmul_workspace_size bytes the tiled matmul may split
+ * the k-steps over several blocks per tile, write fp32 partials there and
+ * add them in a second kernel in split order (the same bits for any grid);
+ * with less it runs unsplit, exactly as miqmm_quantized_matmul.  The call
+ * only reads and writes the workspace on `stream`: the caller keeps it alive
+ * until the work completes (a workspace captured into a graph stays in use
+ * by every replay) and must not share it between calls that may overlap.
+ * No reference counterpart beyond quantized_matmul itself: the caller that
+ * can pass scratch memory for the prefill-sized products.
+ */
+int miqmm_quantized_matmul_ws(void* y, const void* x, const uint32_t* w, const void* scales,
+                              const void* biases, const void* bias, int64_t M, int64_t N, int64_t K,
+                              int transpose, int group_size, int bits, int x_dtype, int sb_dtype,
+                              int y_dtype, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * QuantizedLinear forward: y = quantized_matmul(...) rounded to y_dtype, then
@@ -202,10 +238,10 @@ int miqmm_unpack(uint8_t* codes, const uint32_t* w, int64_t N, int64_t K, int bi
  * only, no GPU access).  route_out: a miqmm_route.  tile_out[4]:
  * qmv -> {16-row tiles per block, M tile, waves per block, 0};
  * qmv_dot -> {rows per lane group, M tile, lanes per row, 0};
- * qmm -> {BM, BN, BK, k ranges} (k ranges > 1: the k-steps are split over
- * that many blocks per output tile, whose fp32 partials are summed in a
- * library-held workspace of the stream; the unsplit kernel runs when it
- * cannot be allocated, e.g. under stream capture).
+ * qmvs -> {rows per block, K-slices (waves) per block, blocks, 0};
+ * qmm -> {BM, BN, BK, k ranges} (k ranges > 1: with a large enough
+ * workspace, miqmm_quantized_matmul_ws splits the k-steps over that many
+ * blocks per output tile; miqmm_quantized_matmul never splits).
  * No reference counterpart: reporting for benches and tests.
  */
 int miqmm_query_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, int* route_out,

@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "miqmm", "libmiqmm.so")
-SOURCES = ["qmv.hip", "checkpoint.cpp", "qmv_mfma.hip", "qmvx.hip", "qmm.hip", "aux.hip", "api.cpp"]
+SOURCES = ["qmv.hip", "checkpoint.cpp", "qmv_mfma.hip", "qmvx.hip", "qmm.hip", "qmvs.hip", "aux.hip", "api.cpp"]
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",

@@ -4,6 +4,7 @@
 // (src/engine/mlx_lm/utils/moe.rs:66-76: nonzero status, message on the side).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -11,6 +12,25 @@
 
 #include "../../include/miqmm.h"
 #include "miqmm_internal.h"
+
+namespace miqmm {
+
+int num_cus() {
+    // per device id: 0 = not queried yet; two threads racing both store the same value
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+}  // namespace miqmm
 
 namespace {
 
@@ -33,6 +53,7 @@ int ok() {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
 constexpr int64_t kMaxDim = (int64_t)1 << 31;
 // selections per expert (on average) from which gather_qmm groups them by
@@ -72,14 +93,21 @@ int check_launch(hipError_t e, const char* what) {
     return ok();
 }
 
+// Rows of at least this many codes take the K-sliced GEMV at M = 1 (one
+// wave per 1 KiB slice of codes; shorter rows would leave most lanes idle)
+constexpr int64_t kMinSlicedK = 2048;
+
 // Measured on MI355X (4-bit g64, cold weights):
-//   M = 1: the v_dot2 GEMV, except for many-row, short-K heads (lm_head 896 ->
+//   M = 1, K >= 2048: the K-sliced GEMV (4096 -> 14336: 7.9 us against 9.2 us);
+//   M = 1, shorter rows: the v_dot2 GEMV, except for many-row, short-K heads (lm_head 896 ->
 //          151936: 18.8 us against 22.8 us), where the LDS-staged MFMA GEMV wins;
 //   2 <= M <= 4: the LDS-staged MFMA GEMV (14336 x 4096: 12.8 / 16.0 us at
 //          M = 2 / 4 against 15.1 / 22.2 us for v_dot2) when it supports the shape;
 //   5 <= M <= 16: the group-diagonal MFMA GEMV, whose cost barely grows with M;
 //   larger M: the tiled MFMA matmul.
-int auto_route(int64_t M, int64_t N, int64_t K, int group_size) {
+int auto_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, bool sb_aligned4 = true) {
+    if (M == 1 && K >= kMinSlicedK && sb_aligned4 && miqmm::qmvs_supported(M, N, K, bits, group_size))
+        return MIQMM_ROUTE_QMVS;
     if (M == 1) {
         const bool wide_head = N >= 65536 && K <= 2048 && miqmm::qmvx_supported(M, K, group_size);
         return wide_head ? MIQMM_ROUTE_QMVX : MIQMM_ROUTE_QMV_DOT;
@@ -103,8 +131,14 @@ int check_args(void* y, const void* x, const uint32_t* w, const void* scales, co
     if (y_dtype != MIQMM_DT_BF16 && y_dtype != MIQMM_DT_F16 && y_dtype != MIQMM_DT_F32)
         return fail(MIQMM_EINVAL, "y dtype %d invalid", y_dtype);
     if (route != MIQMM_ROUTE_AUTO && route != MIQMM_ROUTE_QMV && route != MIQMM_ROUTE_QMM &&
-        route != MIQMM_ROUTE_QMV_DOT && route != MIQMM_ROUTE_QMVX)
+        route != MIQMM_ROUTE_QMV_DOT && route != MIQMM_ROUTE_QMVX && route != MIQMM_ROUTE_QMVS)
         return fail(MIQMM_EINVAL, "route %d invalid", route);
+    if (route == MIQMM_ROUTE_QMVS && M > 1)
+        return fail(MIQMM_ENOTSUP, "route qmvs takes one row of x (M <= 1)");
+    if (route == MIQMM_ROUTE_QMVS && !miqmm::qmvs_supported(1, N, K, bits, group_size))
+        return fail(MIQMM_ENOTSUP, "route qmvs needs K*bits/8 <= 15 KiB and an even K/group_size");
+    if (route == MIQMM_ROUTE_QMVS && M > 0 && (!aligned4(scales) || !aligned4(biases)))
+        return fail(MIQMM_ENOTSUP, "route qmvs needs 4-byte aligned scales and biases");
     if (route == MIQMM_ROUTE_QMVX && !miqmm::qmvx_supported(M < 4 ? M : 4, K, group_size))
         return fail(MIQMM_ENOTSUP, "route qmvx needs K/group_size even and min(M,4)*K <= 32768");
     if (M == 0) {
@@ -119,9 +153,12 @@ int check_args(void* y, const void* x, const uint32_t* w, const void* scales, co
     return ok();
 }
 
+// workspace: fp32 partials for the tiled matmul's k split (nullptr / 0 bytes:
+// the plan never splits)
 int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
                const void* bias, int64_t M, int64_t N, int64_t K, int transpose, int group_size,
-               int bits, int x_dtype, int sb_dtype, int y_dtype, int route, void* stream) {
+               int bits, int x_dtype, int sb_dtype, int y_dtype, int route, void* stream,
+               void* workspace = nullptr, int64_t workspace_bytes = 0) {
     bool noop;
     int st = check_args(y, x, w, scales, biases, M, N, K, transpose, group_size, bits, x_dtype, sb_dtype, y_dtype,
                         route, &noop);
@@ -129,7 +166,8 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
 
     miqmm::QmmArgs a{y, x, w, scales, biases, bias, M, N, K, group_size, bits, x_dtype, sb_dtype, y_dtype,
                      reinterpret_cast<hipStream_t>(stream)};
-    if (route == MIQMM_ROUTE_AUTO) route = auto_route(M, N, K, group_size);
+    if (route == MIQMM_ROUTE_AUTO) route = auto_route(M, N, K, group_size, bits, aligned4(scales) && aligned4(biases));
+    if (route == MIQMM_ROUTE_QMVS) return check_launch(miqmm::launch_qmvs(a), "qmvs launch");
     if (route == MIQMM_ROUTE_QMV || route == MIQMM_ROUTE_QMV_DOT || route == MIQMM_ROUTE_QMVX) {
         // the GEMV kernels handle at most 16 (qmvx: 4) rows of x per pass over W
         const int64_t step = route == MIQMM_ROUTE_QMVX ? 4 : 16;
@@ -147,8 +185,22 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
         }
         return ok();
     }
-    return check_launch(miqmm::launch_qmm(a), "qmm launch");
+    return check_launch(miqmm::launch_qmm(a, workspace, workspace_bytes), "qmm launch");
 }
+
+// bytes of k-split partials the auto route takes for a shape (0: none)
+int64_t split_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
+    if (auto_route(M, N, K, group_size, bits) != MIQMM_ROUTE_QMM) return 0;
+    miqmm::QmmArgs a{};
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.group_size = group_size;
+    a.bits = bits;
+    return miqmm::qmm_workspace_bytes(a);
+}
+
+
 
 // gather_qmm: validation, then the expert-grouped tiled matmul when a
 // workspace is given and there are enough selections per expert to fill its
@@ -232,6 +284,28 @@ int miqmm_quantized_linear(void* y, const void* x, const uint32_t* w, const void
     return qmm_common(y, x, w, scales, biases, bias, M, N, K, 1, group_size, bits, x_dtype, sb_dtype,
                       y_dtype, MIQMM_ROUTE_AUTO, stream);
 }
+
+int miqmm_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                                          int64_t* bytes) {
+    if (!bytes) return fail(MIQMM_EINVAL, "null pointer argument");
+    int st = check_quant(N, K, group_size, bits, MIQMM_DT_BF16);
+    if (st != MIQMM_OK) return st;
+    if (M < 0 || M >= kMaxDim) return fail(MIQMM_EINVAL, "M must be in [0, 2^31), got %lld", (long long)M);
+    *bytes = M == 0 ? 0 : split_workspace_bytes(M, N, K, group_size, bits);
+    return ok();
+}
+
+int miqmm_quantized_matmul_ws(void* y, const void* x, const uint32_t* w, const void* scales, const void* biases,
+                              const void* bias, int64_t M, int64_t N, int64_t K, int transpose, int group_size,
+                              int bits, int x_dtype, int sb_dtype, int y_dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+    if (workspace_bytes < 0) return fail(MIQMM_EINVAL, "workspace_bytes must be >= 0");
+    if (workspace && !aligned16(workspace)) return fail(MIQMM_EINVAL, "workspace must be 16-byte aligned");
+    return qmm_common(y, x, w, scales, biases, bias, M, N, K, transpose, group_size, bits, x_dtype, sb_dtype,
+                      y_dtype, MIQMM_ROUTE_AUTO, stream, workspace, workspace ? workspace_bytes : 0);
+}
+
+
 
 int miqmm_quantized_matmul_grouped(const miqmm_problem* problems, int count, int64_t M, int64_t K,
                                    int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
@@ -360,13 +434,14 @@ int miqmm_query_route(int64_t M, int64_t N, int64_t K, int group_size, int bits,
     a.K = K;
     a.group_size = group_size;
     a.bits = bits;
-    const int route = M == 0 ? MIQMM_ROUTE_QMV_DOT : auto_route(M, N, K, group_size);
+    const int route = M == 0 ? MIQMM_ROUTE_QMV_DOT : auto_route(M, N, K, group_size, bits);
     if (route_out) *route_out = route;
     if (tile_out) {
         tile_out[0] = tile_out[1] = tile_out[2] = tile_out[3] = 0;
         if (route == MIQMM_ROUTE_QMV) miqmm::qmv_mfma_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
         else if (route == MIQMM_ROUTE_QMVX) miqmm::qmvx_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
         else if (route == MIQMM_ROUTE_QMV_DOT) miqmm::qmv_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
+        else if (route == MIQMM_ROUTE_QMVS) miqmm::qmvs_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
         else miqmm::qmm_config(a, &tile_out[0], &tile_out[1], &tile_out[2], &tile_out[3]);
     }
     return ok();

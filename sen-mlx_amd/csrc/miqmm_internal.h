@@ -60,7 +60,11 @@ bool qmv_ksplit(int64_t M, int64_t N, int64_t K, int bits);
 hipError_t launch_qmv_gather(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_expert,
                              int64_t experts, int64_t x_stride, int64_t y_stride);
 hipError_t launch_qmv_mfma(const QmmArgs& a);  // group-diagonal MFMA GEMV
-hipError_t launch_qmm(const QmmArgs& a);
+// workspace: fp32 partials of a k split (the plan splits only where
+// workspace_bytes holds them; nullptr / 0: never split)
+hipError_t launch_qmm(const QmmArgs& a, void* workspace = nullptr, int64_t workspace_bytes = 0);
+// workspace bytes the qmm plan's k split takes for this shape (0: unsplit)
+int64_t qmm_workspace_bytes(const QmmArgs& a);
 // expert grouping of gather_qmm's selections (M = 1 per selection): the
 // workspace (gather_grouped_workspace bytes) holds, per expert, its range of
 // the selection list, and the list of tiles of up to `tr` selections of one
@@ -86,13 +90,22 @@ hipError_t launch_gather_grouped(const QmmArgs& a, const int32_t* idx, int64_t T
 hipError_t launch_gather_gemv(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_index,
                               int64_t experts, int64_t x_bytes, void* workspace);
 hipError_t launch_qmvx(const QmmArgs& a);      // MFMA GEMV, M <= 4, x in LDS
+hipError_t launch_qmvs(const QmmArgs& a);      // K-sliced v_dot2 GEMV, M == 1
+// M == 1, at most 15 K-slices, an even number of groups per row (the scale
+// and bias pointers must also be 4-byte aligned, checked by the caller)
+bool qmvs_supported(int64_t M, int64_t N, int64_t K, int bits, int group_size);
+// compute units of the current device (queried once per device): the GEMV
+// grids are sized by it
+int num_cus();
 bool qmvx_supported(int64_t M, int64_t K, int group_size);
 
 // tiling used for a given problem; for reporting
 void qmv_config(const QmmArgs& a, int* rows_per_subgroup, int* m_tile, int* lanes_per_row);
 void qmv_mfma_config(const QmmArgs& a, int* tiles_per_block, int* m_tile, int* waves_per_block);
-void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk, int* ks);  // ks: k ranges (split when > 1)
+// ks: k ranges of the plan given a large enough workspace (split when > 1)
+void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk, int* ks);
 void qmvx_config(const QmmArgs& a, int* m_tile, int* k_splits, int* stage_codes);
+void qmvs_config(const QmmArgs& a, int* rows_per_block, int* slices, int* blocks);
 
 hipError_t launch_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,
                              int64_t N, int64_t K, int group_size, int bits, int sb_dtype,

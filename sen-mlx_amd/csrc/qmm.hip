@@ -35,7 +35,6 @@
 // which dequantizes W tiles into threadgroup memory in the activation type.
 #include <algorithm>
 #include <atomic>
-#include <mutex>
 
 #include "miqmm_device.h"
 #include "miqmm_internal.h"
@@ -124,13 +123,12 @@ struct QmmGather {
 };
 
 // Split of the k-steps over gridDim.z blocks per output tile (ks > 1): each
-// block writes its fp32 partial tile to part[z], then counts itself in on
-// the tile's counter; the last block to arrive adds the other partials to
-// its own and writes the output, and resets the counter to zero.
+// block writes its fp32 partial tile to part[z]; a second kernel
+// (qmm_split_reduce_kernel) adds the ks partials of every output in split
+// order and writes y.  The partials live in a workspace the caller owns.
 struct QmmSplit {
-    float* part;   // [ks][M][N] fp32 partial sums
-    int32_t* cnt;  // one arrival counter per output tile, zero between launches
-    int ks;        // number of k ranges (1: no split)
+    float* part;  // [ks][M][N] fp32 partial sums
+    int ks;       // number of k ranges (1: no split)
 };
 
 // fp32 partials are written and read at device scope (cache policy SC1:
@@ -437,8 +435,7 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
     float* stage = reinterpret_cast<float*>(smem) + wid * 32 * ES;
     const int wrow0 = m0 + wm * WM, wcol0 = n0 + wn * WN;
     const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
-    constexpr int FLAG = (int)qmm_lds_bytes<BITS, BN>() - 16;  // LDS word for the last-arrival flag
-    static_assert(NW * 32 * ES * 4 <= FLAG, "epilogue staging below the flag");
+    static_assert(NW * 32 * ES * 4 <= (int)qmm_lds_bytes<BITS, BN>(), "epilogue staging fits");
     // unsplit: the output; split: this block's fp32 partial tile -> part[z]
     const bool partial = sp.ks > 1;
     {
@@ -508,68 +505,48 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
             __builtin_amdgcn_wave_barrier();  // reads of this band before the next band's writes
         }
     }
-    if (!partial) return;
-    // every partial store of this block has completed (device-scope stores
-    // count in vmcnt until they reach the coherent level), then count in
-    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
-    __syncthreads();
-    int* flag = reinterpret_cast<int*>(smem + FLAG);
-    if (tid == 0) {
-        int32_t* c = sp.cnt + blockIdx.y * gridDim.x + blockIdx.x;
-        const int last = atomicAdd(c, 1) == sp.ks - 1;
-        if (last) *c = 0;  // every split has counted in: ready for the next launch
-        *flag = last;
+}
+
+// y = sum over z of part[z] (z = 0 .. ks-1 in order, the same bits for any
+// grid), rounded to y's dtype (+ bias as a separate rounding): one thread per
+// run of 8 outputs of a row
+__global__ __launch_bounds__(256) void qmm_split_reduce_kernel(const float* __restrict__ part, int ks, int M, int N,
+                                                               void* __restrict__ y, const void* __restrict__ bias,
+                                                               int y_dtype) {
+    const int runs = (N + 7) / 8;
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (int64_t)M * runs) return;
+    const int gr = (int)(q / runs), gc = (int)(q % runs) * 8;
+    const int64_t o = (int64_t)gr * N + gc;
+    const int64_t plane = (int64_t)M * N;
+    const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int z = 0; z < ks; ++z) {
+        const float* p = part + z * plane + o;
+        if (vec) {
+            const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p), b = *reinterpret_cast<const f32x4_t*>(p + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] += a[e];
+                v[4 + e] += b[e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (gc + e < N) v[e] += p[e];
+        }
     }
-    __syncthreads();
-    if (!*flag) return;  // block-uniform
-    // the last block to arrive sums the ks partials of the tile in split
-    // order (the same result whichever block is last) and writes the output;
-    // four runs of 8 outputs per thread in flight at a time
-    constexpr int RUNS_T = BN / 8;
-    const auto pr = make_rsrc(sp.part, (uint32_t)min((int64_t)sp.ks * M * N * 4, (int64_t)0xFFFFFFF0));
-#pragma unroll 1
-    for (int q0 = tid; q0 < kBM * RUNS_T; q0 += 4 * NT) {
-        f32x4_t a0[4], a1[4];
+    if (vec && y_dtype != DT_F32) {
+        u32x4_t h;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) a0[u] = a1[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-        for (int z = 0; z < sp.ks; ++z) {
+        for (int e = 0; e < 4; ++e)
+            h[e] = (uint32_t)out_half_bits(y_dtype, v[2 * e], bias, gc + 2 * e) |
+                   ((uint32_t)out_half_bits(y_dtype, v[2 * e + 1], bias, gc + 2 * e + 1) << 16);
+        *reinterpret_cast<u32x4_t*>((uint16_t*)y + o) = h;
+    } else {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int q = q0 + u * NT, gr = m0 + q / RUNS_T, gc = n0 + (q % RUNS_T) * 8;
-                if (q >= kBM * RUNS_T || gr >= M || gc >= N) continue;
-                const uint32_t po = (uint32_t)(((int64_t)z * M * N + (int64_t)gr * N + gc) * 4);
-                if (vec) {
-                    a0[u] += part_load4(pr, po);
-                    a1[u] += part_load4(pr, po + 16);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (gc + e < N) a0[u][e] += part_load1(pr, po + 4 * e);
-                        if (gc + 4 + e < N) a1[u][e] += part_load1(pr, po + 16 + 4 * e);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int q = q0 + u * NT, gr = m0 + q / RUNS_T, gc = n0 + (q % RUNS_T) * 8;
-            if (q >= kBM * RUNS_T || gr >= M || gc >= N) continue;
-            const int64_t o = (int64_t)gr * N + gc;
-            const float v[8] = {a0[u][0], a0[u][1], a0[u][2], a0[u][3], a1[u][0], a1[u][1], a1[u][2], a1[u][3]};
-            if (vec && y_dtype != DT_F32) {
-                u32x4_t h;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    h[e] = (uint32_t)out_half_bits(y_dtype, v[2 * e], bias, gc + 2 * e) |
-                           ((uint32_t)out_half_bits(y_dtype, v[2 * e + 1], bias, gc + 2 * e + 1) << 16);
-                *reinterpret_cast<u32x4_t*>((uint16_t*)y + o) = h;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (gc + e < N) store_out(y, o + e, y_dtype, v[e], bias, gc + e);
-            }
-        }
+        for (int e = 0; e < 8; ++e)
+            if (gc + e < N) store_out(y, o + e, y_dtype, v[e], bias, gc + e);
     }
 }
 
@@ -637,11 +614,11 @@ __global__ __launch_bounds__(1024) void gather_plan_kernel(const int32_t* idx, i
 }
 
 // Tile width and k split by a rounds model of MI355X: tiles run in rounds
-// of one block per CU (256 CUs); a 128-wide tile (four waves) over K takes
-// about 0.0202 us per unit of K, a 256-wide one (eight waves) 1.3x that; a
-// split into ks k ranges divides the tile time by ks and adds the partial
-// traffic, (2 ks - 1) fp32 values per output at a measured 1.6 TB/s
-// effective.  E.g. M = 2048: N = 14336 and 6144 -> 256 wide, N = 4096 ->
+// of one block per CU; a 128-wide tile (four waves) over K takes about
+// 0.0202 us per unit of K, a 256-wide one (eight waves) 1.3x that; a split
+// into ks k ranges divides the tile time by ks and adds the partial traffic
+// (ks fp32 values per output written, then read back by the reduce kernel,
+// at a measured 1.6 TB/s effective) and the reduce kernel's launch.  E.g. M = 2048: N = 14336 and 6144 -> 256 wide, N = 4096 ->
 // 128 wide at K = 4096 and 256 wide in two k ranges at K = 14336; M = 256,
 // N = 4096, K = 4096 -> 128 wide in four k ranges.
 struct QmmPlan {
@@ -650,15 +627,16 @@ struct QmmPlan {
 
 QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int max_ks) {
     const int64_t mt = (M + kBM - 1) / kBM, KT = (K + kBK - 1) / kBK;
+    const int64_t cus = num_cus();
     QmmPlan best{128, 1};
     double best_us = 1e300;
     for (int bn : {128, 256}) {
         const int64_t tiles = mt * ((N + bn - 1) / bn);
         for (int ks = 1; ks <= max_ks; ++ks) {
             if (ks > 1 && (KT < 8 * ks || (double)ks * M * N * 4 >= 2147483648.0)) break;  // >= 8 k-steps per range
-            const double rounds = (double)((tiles * ks + 255) / 256);
+            const double rounds = (double)((tiles * ks + cus - 1) / cus);
             double us = rounds * (bn == 256 ? 1.3 : 1.0) * 0.0202 * (double)K / ks;
-            if (ks > 1) us += (double)M * N * 4 * (2 * ks - 1) / 1.6e6;
+            if (ks > 1) us += (double)M * N * 4 * (2 * ks) / 1.6e6 + 2.0;
             if (us < best_us) {
                 best_us = us;
                 best = {bn, ks};
@@ -670,84 +648,43 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int max_ks) {
 
 constexpr int kMaxSplit = 4;
 
-// The split path's device workspace per (device, stream): tile counters
-// (zero between launches: each tile's last block resets its own) followed by
-// the fp32 partials.  Allocated or grown only outside stream capture; when
-// it cannot be had the caller runs unsplit.  One table entry per stream, so
-// calls on different streams never share counters or partials.
-struct SplitWs {
-    int device;
-    hipStream_t stream;
-    char* ptr;
-    size_t cnt_bytes, part_bytes;
-};
-std::mutex g_split_mu;
-SplitWs g_split[8];
-int g_split_n = 0;
-
-bool split_workspace(hipStream_t stream, size_t cnt_bytes, size_t part_bytes, QmmSplit& sp) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return false;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return false;
-    std::lock_guard<std::mutex> lock(g_split_mu);
-    SplitWs* e = nullptr;
-    for (int i = 0; i < g_split_n; ++i)
-        if (g_split[i].device == dev && g_split[i].stream == stream) e = &g_split[i];
-    if (!e || e->cnt_bytes < cnt_bytes || e->part_bytes < part_bytes) {
-        if (cs != hipStreamCaptureStatusNone) return false;
-        if (!e) {
-            if (g_split_n == 8) return false;
-            e = &g_split[g_split_n++];
-            *e = {dev, stream, nullptr, 0, 0};
-        }
-        if (e->ptr) {  // the old buffer may still be in use by this stream's kernels
-            if (hipStreamSynchronize(stream) != hipSuccess) return false;
-            (void)hipFree(e->ptr);
-            e->ptr = nullptr;
-        }
-        const size_t cb = (std::max(cnt_bytes, e->cnt_bytes) + 255) / 256 * 256;
-        const size_t pb = (std::max(part_bytes, e->part_bytes) + 255) / 256 * 256;
-        e->cnt_bytes = e->part_bytes = 0;
-        if (hipMalloc(&e->ptr, cb + pb) != hipSuccess) {
-            e->ptr = nullptr;
-            (void)hipGetLastError();
-            return false;
-        }
-        if (hipMemsetAsync(e->ptr, 0, cb, stream) != hipSuccess) return false;
-        e->cnt_bytes = cb;
-        e->part_bytes = pb;
-    }
-    sp.cnt = reinterpret_cast<int32_t*>(e->ptr);
-    sp.part = reinterpret_cast<float*>(e->ptr + e->cnt_bytes);
-    return true;
+// the plan with k ranges only where `workspace_bytes` holds their partials
+QmmPlan plan_with_workspace(const QmmArgs& a, int64_t workspace_bytes) {
+    QmmPlan pl = plan_qmm(a.M, a.N, a.K, kMaxSplit);
+    if (pl.ks > 1 && (double)pl.ks * a.M * a.N * 4 > (double)workspace_bytes) pl = plan_qmm(a.M, a.N, a.K, 1);
+    return pl;
 }
 
 template <int BITS, int SBT>
-hipError_t launch_bn(const QmmArgs& a) {
+hipError_t launch_bn(const QmmArgs& a, void* workspace, int64_t workspace_bytes) {
     const QmmGather none{};
     const int64_t mt = (a.M + kBM - 1) / kBM;
-    QmmPlan pl = plan_qmm(a.M, a.N, a.K, kMaxSplit);
-    QmmSplit sp{nullptr, nullptr, 1};
-    if (pl.ks > 1) {
-        const int64_t tiles = mt * ((a.N + pl.bn - 1) / pl.bn);
-        if (split_workspace(a.stream, (size_t)tiles * 4, (size_t)pl.ks * a.M * a.N * 4, sp)) sp.ks = pl.ks;
-        else pl = plan_qmm(a.M, a.N, a.K, 1);
-    }
-    return pl.bn == 256 ? launch_t<BITS, SBT, 256, false>(a, none, mt, sp)
-                        : launch_t<BITS, SBT, 128, false>(a, none, mt, sp);
+    const QmmPlan pl = plan_with_workspace(a, workspace ? workspace_bytes : 0);
+    const QmmSplit sp{static_cast<float*>(workspace), pl.ks};
+    hipError_t e = pl.bn == 256 ? launch_t<BITS, SBT, 256, false>(a, none, mt, sp)
+                                : launch_t<BITS, SBT, 128, false>(a, none, mt, sp);
+    if (e != hipSuccess || pl.ks == 1) return e;
+    const int64_t threads = a.M * ((a.N + 7) / 8);
+    hipLaunchKernelGGL(qmm_split_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a.stream,
+                       static_cast<const float*>(workspace), pl.ks, (int)a.M, (int)a.N, a.y, a.bias, a.y_dtype);
+    return hipGetLastError();
 }
 
 template <int BITS, int SBT>
 hipError_t launch_gather_bn(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles) {
     // the expert-grouped grid has as many M tiles as experts or more: 128-wide
     // tiles fill the chip whenever 256-wide ones would not
-    const QmmSplit unsplit{nullptr, nullptr, 1};
+    const QmmSplit unsplit{nullptr, 1};
     return plan_qmm(kBM * m_tiles, a.N, a.K, 1).bn == 256 ? launch_t<BITS, SBT, 256, true>(a, gq, m_tiles, unsplit)
                                                          : launch_t<BITS, SBT, 128, true>(a, gq, m_tiles, unsplit);
 }
 
 }  // namespace
+
+int64_t qmm_workspace_bytes(const QmmArgs& a) {
+    const QmmPlan pl = plan_qmm(a.M, a.N, a.K, kMaxSplit);
+    return pl.ks > 1 ? (int64_t)pl.ks * a.M * a.N * 4 : 0;
+}
 
 void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk, int* ks) {
     const QmmPlan pl = plan_qmm(a.M, a.N, a.K, kMaxSplit);
@@ -757,9 +694,12 @@ void qmm_config(const QmmArgs& a, int* bm, int* bn, int* bk, int* ks) {
     if (ks) *ks = pl.ks;
 }
 
-hipError_t launch_qmm(const QmmArgs& a) {
-    if (a.bits == 4) return a.sb_dtype == DT_F16 ? launch_bn<4, DT_F16>(a) : launch_bn<4, DT_BF16>(a);
-    return a.sb_dtype == DT_F16 ? launch_bn<8, DT_F16>(a) : launch_bn<8, DT_BF16>(a);
+hipError_t launch_qmm(const QmmArgs& a, void* workspace, int64_t workspace_bytes) {
+    if (a.bits == 4)
+        return a.sb_dtype == DT_F16 ? launch_bn<4, DT_F16>(a, workspace, workspace_bytes)
+                                    : launch_bn<4, DT_BF16>(a, workspace, workspace_bytes);
+    return a.sb_dtype == DT_F16 ? launch_bn<8, DT_F16>(a, workspace, workspace_bytes)
+                                : launch_bn<8, DT_BF16>(a, workspace, workspace_bytes);
 }
 
 int64_t gather_grouped_max_tiles(int64_t S, int64_t E, int tr) { return S / tr + E + 1; }

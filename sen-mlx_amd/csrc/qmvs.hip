@@ -1,0 +1,468 @@
+// qmvs.hip -- K-sliced GEMV for one row of x (M = 1) over long rows.
+//
+//   y[n] = sum_k x[k] * (s[n, k/g] * q[n, k] + b[n, k/g])             (transpose=true)
+//
+// The decode-time call of every large quantized projection of the reference
+// (src/engine/mlx_lm/models/llama.rs:195-197,249,293-294 with x [1, 1, K]).
+//
+// HBM-bound design (no MFMA).  A row of W is cut into K-slices of 1 KiB of
+// codes (2048 4-bit or 1024 8-bit codes).  A block covers RB consecutive rows
+// with one wave per K-slice; lane l of wave w owns the 16-byte chunk l of
+// slice w in each of the block's rows.  A wave runs straight through, with
+// no loop:
+//   - it loads its x chunk (the same for every row it computes), then issues
+//     the scales and biases of its RB rows (one 1 KiB run per row stride,
+//     copied straight to the wave's LDS by direct-to-LDS loads) and the
+//     codes of its RB rows (each load instruction 1 KiB contiguous bytes of
+//     one row), so everything the wave reads is in flight at once;
+//   - it prepares x once (the bf16 pairs the code unpack needs, and its
+//     sum) while the codes are in flight, then computes the rows in order as
+//     they land (the compiler waits for each row's codes on its own);
+//   - it reduces its lanes' partial sums of all its rows at once (a
+//     transposed reduction: lane-half swaps, then DPP); wave 0 adds the
+//     K-slices' partials through LDS in slice order and writes the outputs.
+// The grid has one block per RB rows: a chip-full of waves runs at once and
+// later blocks take the CUs as earlier ones finish.  Load instructions that
+// read nothing are not issued: out-of-range loads still take a slot in the
+// CU's memory pipeline, which is what the kernel's time is made of.
+// The arithmetic per chunk is the exact factorised dequant of the other
+// GEMVs: sum_k x_k (s q_k + b) = s * sum_k x_k q_k + b * sum_k x_k, with the
+// codes made exact 16-bit float operands by one and-or with a magic
+// exponent: 4-bit codes as fp16 1024 + q (bits 0-3) or 1024 + 16 q (bits
+// 4-7), one shift per word of eight codes, against x scaled per lane by an
+// exact power of two (and by 1/16 for the second kind) into fp16; 8-bit
+// codes as the bf16 top half of their fp32 value against bf16 x.  The
+// offsets and scales are undone per row in fp32:
+//   sum_k x_k q_k = 2^E (dot - 1024 * sum of the x operands).
+// Measured on MI355X (cold weights, back-to-back graph launches, 4-bit g64):
+// M = 1, 4096 -> 14336 and 14336 -> 4096 in 7.9 us (4.2 TB/s) against 9.2 and
+// 9.9 us for the v_dot2 GEMV; the 5376 -> 262144 head in 113 us (7.0 TB/s);
+// a bare streaming read of the same 33 MB takes 5.9 us.
+#include <type_traits>
+
+#include "miqmm_device.h"
+#include "miqmm_internal.h"
+
+namespace miqmm {
+namespace {
+
+constexpr int kSliceBytes = 1024;  // codes per K-slice: 64 lanes x 16 bytes
+
+// cache policy of the output stores (0: default; measured on MI355X, a
+// non-temporal store per block added 3.5 us to a 6 us streaming read)
+#ifndef QMVS_STORE_POLICY
+#define QMVS_STORE_POLICY 0
+#endif
+
+// fp16 operands for the 4-bit unpack (codes at bits 0-3 and 4-7 of each
+// half are exact fp16 mantissas, one shift per word fewer than bf16)
+#ifndef QMVS_F16
+#define QMVS_F16 1
+#endif
+typedef __attribute__((ext_vector_type(2))) _Float16 half2_t;
+
+// s_waitcnt immediate: vmcnt(n), expcnt and lgkmcnt left unconstrained
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+struct QmvsArgs {
+    const uint16_t* x;
+    const uint32_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+    void* y;
+    const void* bias;
+    int N, K, gs_shift, y_dtype;
+};
+
+// LDS per wave: scales then biases of its rows, ND KiB each (a direct-to-LDS
+// load moves 1 KiB); after all waves' areas, the slice partials [waves][RB]
+template <int ND>
+constexpr int wave_lds() { return 2 * ND * kSliceBytes; }
+
+// DPP moves (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_ror:8)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sums RB per-lane values v[0..RB) over the wave's 64 lanes, one row per
+// value, as a transposed reduction: lane halves trade values
+// (permlane32_swap), then 16-lane rows (permlane16_swap), then 8- and
+// 4-lane groups (DPP), each exchange halving the values a lane keeps, and
+// the last lanes of a group add what they hold.  Afterwards lane l holds the
+// sum of value l >> (6 - log2 RB): lanes 64/RB * j .. of row j.  About
+// 3 RB instructions for the RB values, against 12 per value for one
+// butterfly per value.
+template <int RB>
+__device__ __forceinline__ float transposed_sum(float (&v)[RB], int lane) {
+    static_assert(RB == 4 || RB == 8 || RB == 16 || RB == 32, "rows per reduction");
+    constexpr int H = RB / 2;
+    float b[H];
+#pragma unroll
+    for (int j = 0; j < H; ++j) {  // lanes 0-31: value j, lanes 32-63: value j + H
+        const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + H]), false,
+                                                        false);
+        b[j] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+    }
+    constexpr int Q = H / 2;
+    float c[Q];
+#pragma unroll
+    for (int j = 0; j < Q; ++j) {  // 16-lane row G: value j + (G & 1) Q + (G >> 1) H
+        const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(b[j]), __float_as_uint(b[j + Q]), false,
+                                                        false);
+        c[j] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+    }
+    float r;
+    if constexpr (RB == 4) {
+        r = c[0];  // value l >> 4: sum its 16 lanes
+        r += dpp<0xB1>(r);
+        r += dpp<0x4E>(r);
+        r += dpp<0x141>(r);
+        r += dpp<0x128>(r);
+    } else {
+        // halves of 8 lanes within each 16-lane row (row_ror:8 pairs lane l with l ^ 8)
+        const bool hi8 = (lane & 8) != 0;
+        constexpr int E = Q / 2 > 0 ? Q / 2 : 1;
+        float d[E];
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            const float keep = hi8 ? c[j + E] : c[j], give = hi8 ? c[j] : c[j + E];
+            d[j] = keep + dpp<0x128>(give);
+        }
+        if constexpr (RB == 8) {
+            r = d[0];  // value l >> 3: sum its 8 lanes
+            r += dpp<0xB1>(r);
+            r += dpp<0x4E>(r);
+            r += dpp<0x141>(r);
+        } else {
+            // lanes l and 7 - l of each 8 (row_half_mirror) hold the same values
+            const bool hi4 = (lane & 4) != 0;
+            constexpr int F = E / 2;
+            float f[F];
+#pragma unroll
+            for (int j = 0; j < F; ++j) {
+                const float keep = hi4 ? d[j + F] : d[j], give = hi4 ? d[j] : d[j + F];
+                f[j] = keep + dpp<0x141>(give);
+            }
+            if constexpr (RB == 16) {
+                r = f[0];  // value l >> 2: sum its 4 lanes
+                r += dpp<0xB1>(r);
+                r += dpp<0x4E>(r);
+            } else {
+                // lanes l and l ^ 2 (quad_perm [2,3,0,1]) hold the same two values
+                const bool hi2 = (lane & 2) != 0;
+                const float keep = hi2 ? f[1] : f[0], give = hi2 ? f[0] : f[1];
+                r = keep + dpp<0x4E>(give);  // value l >> 1: sum its 2 lanes
+                r += dpp<0xB1>(r);
+            }
+        }
+    }
+    return r;
+}
+
+// RB rows per block; ND direct-to-LDS loads per scale (and bias) array:
+// RB * (bytes of scales per row and slice) / 1 KiB, rounded up
+template <int RB>
+constexpr int max_threads() { return RB >= 32 ? 512 : 1024; }  // 32 rows of codes take 128 registers
+
+template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS>
+__global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const QmvsArgs P) {
+    constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk: 32 or 16
+    constexpr int CPC = 1 << CPC_SHIFT;
+    constexpr int NP = CPC / 2;                   // bf16 pairs of x per chunk
+    constexpr int XQ = NP / 4;                    // 16-byte x loads per chunk
+
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int lane = threadIdx.x & 63;
+    const int ws = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's K-slice
+    const int KS = blockDim.x >> 6;
+    const int K = P.K, gs_shift = P.gs_shift;
+    const int C = K >> CPC_SHIFT;       // chunks per row
+    const int c = ws * 64 + lane;       // this lane's chunk of every row
+    const bool cv = c < C;
+    const uint32_t row_bytes = (uint32_t)K * BITS / 8;
+    const int G = K >> gs_shift;
+    const int r0 = blockIdx.x * RB;
+    const int nrows = min(RB, P.N - r0);
+    constexpr int ysz = YF32 ? 4 : 2;
+
+    // x chunk of this lane (zero past the row end); prepared below, once the
+    // codes are in flight
+    uint32_t xw[NP];
+    {
+        const auto xr = make_rsrc(P.x, (uint32_t)K * 2);
+#pragma unroll
+        for (int i = 0; i < XQ; ++i) {
+            const u32x4_t v = bload16(xr, cv ? (uint32_t)c * CPC * 2 + i * 16 : kOOB);
+            xw[4 * i + 0] = v[0];
+            xw[4 * i + 1] = v[1];
+            xw[4 * i + 2] = v[2];
+            xw[4 * i + 3] = v[3];
+        }
+    }
+
+    // The loads are issued in this order, fenced against the scheduler: the
+    // x chunk, the direct-to-LDS scales and biases, then the codes (and bias),
+    // so that (1) the explicit wait below, which counts the loads issued after
+    // the scales and biases, is exact, and (2) every code load is in flight
+    // before any arithmetic (left alone, the scheduler sinks the later rows'
+    // loads below the first rows' arithmetic).
+    __builtin_amdgcn_sched_barrier(0);
+    // scales and biases of this wave's slice of the block's rows, to LDS:
+    // row j's gps scales at j * sb (sb = 2 * gps bytes, a multiple of 16);
+    // DMA lane l of load d carries 16 bytes of row (d * 64 + l) / lpr
+    const auto sr = make_rsrc(P.s + (size_t)r0 * G, (uint32_t)nrows * G * 2);
+    const auto br = make_rsrc(P.b + (size_t)r0 * G, (uint32_t)nrows * G * 2);
+    const int gps = (kSliceBytes * 8 / BITS) >> gs_shift;
+    const int sb = 2 * gps;
+    const int lpr_shift = __builtin_ctz((unsigned)sb >> 4);  // DMA lanes per row: a power of two
+    char* const wl = smem + ws * wave_lds<ND>();
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+        const int dl = d * 64 + lane;
+        const int row = dl >> lpr_shift, g0 = ws * gps + (dl & ((1 << lpr_shift) - 1)) * 8;
+        const uint32_t off = row < RB && g0 < G ? ((uint32_t)row * G + g0) * 2 : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(wl + d * kSliceBytes), 16, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (lds_void*)(wl + (ND + d) * kSliceBytes), 16, off, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // codes of the block's rows (rows past the block's last read zero)
+    const auto wr = make_rsrc((const char*)P.w + (size_t)r0 * row_bytes, (uint32_t)nrows * row_bytes);
+    u32x4_t q[RB];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) q[j] = bload16_nt(wr, cv ? (uint32_t)j * row_bytes + (uint32_t)c * 16 : kOOB);
+    // the bias of the row this lane stores: row t of the block by lane t of wave 0
+    const int t_row = lane;
+    const bool t_mine = ws == 0 && lane < nrows;
+    uint32_t bias_bits = 0;
+    if constexpr (BIAS) {
+        const auto biasr = make_rsrc((const char*)P.bias + (size_t)r0 * ysz, (uint32_t)nrows * ysz);
+        const uint32_t boff = t_mine ? (uint32_t)t_row * ysz : kOOB;
+        if constexpr (YF32) bias_bits = __builtin_amdgcn_raw_buffer_load_b32(biasr, boff, 0, 0);
+        else bias_bits = __builtin_amdgcn_raw_buffer_load_b16(biasr, boff, 0, 0);
+    }
+
+    __builtin_amdgcn_sched_barrier(0);
+    // x prepared: pairs (x_j, x_{j+4}) matching the 4-bit unpack, and the sum
+    uint32_t X[NP];
+    float xs = 0.f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) xs = dot2(xw[i], kOnesBf16x2, xs);
+#if QMVS_F16
+    // fp16 operands: x scaled by 2^-E (E: exponent of the chunk's largest
+    // |x|, so every operand is below 2 and exact unless below fp16's normal
+    // range), the operands facing the codes taken at bits 4-7 further by
+    // 1/16; xsc = 2^E and xoff = -2^E * 1024 * (sum of the operands) undo
+    // the scale and the codes' 1024 offset
+    float xsc, xoff;
+    if constexpr (BITS == 4) {
+        uint32_t emax = 0;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) emax = max(emax, max((xw[i] >> 7) & 0xFFu, (xw[i] >> 23) & 0xFFu));
+        const int e = (int)emax - 127;
+        xsc = __builtin_amdgcn_ldexpf(1.f, e);
+        auto h = [&](int k, int extra) {  // x_k of the chunk, scaled, as fp16 bits
+            const uint32_t w = xw[k >> 1];
+            const float f = __uint_as_float((k & 1) ? (w & 0xFFFF0000u) : (w << 16));
+            return (uint32_t)f32_to_f16_bits(__builtin_amdgcn_ldexpf(f, -e - extra));
+        };
+        float ssum = 0.f;
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) {
+            const int k0 = 8 * wi;
+            X[4 * wi + 0] = h(k0 + 0, 0) | (h(k0 + 4, 0) << 16);
+            X[4 * wi + 1] = h(k0 + 1, 4) | (h(k0 + 5, 4) << 16);
+            X[4 * wi + 2] = h(k0 + 2, 0) | (h(k0 + 6, 0) << 16);
+            X[4 * wi + 3] = h(k0 + 3, 4) | (h(k0 + 7, 4) << 16);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                ssum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, X[4 * wi + t]),
+                                              __builtin_bit_cast(half2_t, 0x3C003C00u), ssum, false);
+        }
+        xoff = -xsc * 1024.f * ssum;
+    } else
+#endif
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) perm_x_for4(&xw[4 * wi], &X[4 * wi]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NP; ++i) X[i] = xw[i];
+    }
+
+    // the DMA must land before the stage is read from LDS (the compiler does
+    // not track that dependency): issued after it and still allowed in
+    // flight are the codes (and the bias)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(RB + (BIAS ? 1 : 0)));
+    asm volatile("" ::: "memory");
+
+    const uint32_t kMask = vgpr_const(0x000F000Fu), kMagic = kMagic128x2;
+#if QMVS_F16
+    const uint32_t kMaskHi = vgpr_const(0x00F000F0u);
+#endif
+    // this lane's scale / bias of row j at j * sb + 2 * (group in slice)
+    const uint32_t sl_off = (uint32_t)((lane << CPC_SHIFT) >> gs_shift) * 2;
+    // per-lane partial of every row; in the wave of the slice that runs past
+    // the row end (if any), lanes past it take zero scales and biases, so
+    // they add nothing whatever their LDS holds
+    const bool partial = __builtin_amdgcn_readfirstlane((int)(ws == KS - 1 && (C & 63) != 0)) != 0;
+    float part[RB];
+    auto rows = [&](auto masked) {
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            uint32_t p[NP];
+            float a = 0.f;
+            float s = half_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(wl + j * sb + sl_off));
+            float b = half_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(wl + ND * kSliceBytes + j * sb + sl_off));
+            if constexpr (decltype(masked)::value) {
+                s = cv ? s : 0.f;
+                b = cv ? b : 0.f;
+            }
+#if QMVS_F16
+            if constexpr (BITS == 4) {
+                constexpr uint32_t kMagic1024 = 0x64006400u;  // fp16 1024 | q: exact 1024 + q (and 1024 + 16 q)
+#pragma unroll
+                for (int wi = 0; wi < 4; ++wi) {
+                    const uint32_t w = q[j][wi], w8 = w >> 8;
+                    p[4 * wi + 0] = and_or(w, kMask, kMagic1024);
+                    p[4 * wi + 1] = and_or(w, kMaskHi, kMagic1024);
+                    p[4 * wi + 2] = and_or(w8, kMask, kMagic1024);
+                    p[4 * wi + 3] = and_or(w8, kMaskHi, kMagic1024);
+                }
+#pragma unroll
+                for (int i = 0; i < NP; ++i)
+                    a = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, X[i]), __builtin_bit_cast(half2_t, p[i]),
+                                               a, false);
+                part[j] = fmaf(s, fmaf(a, xsc, xoff), b * xs);
+                continue;
+            }
+#endif
+#pragma unroll
+            for (int wi = 0; wi < 4; ++wi) {
+                if constexpr (BITS == 4) unpack4_magic(q[j][wi], &p[wi * 4], kMask, kMagic);
+                else unpack8_pairs(q[j][wi], &p[wi * 2]);
+            }
+#pragma unroll
+            for (int i = 0; i < NP; ++i) a = dot2(X[i], p[i], a);
+            if constexpr (BITS == 4) b = fmaf(-128.f, s, b);
+            part[j] = fmaf(b, xs, s * a);
+        }
+    };
+    (void)partial;
+    rows(std::true_type{});
+    // the wave's sum of row j lands in lanes (64 / RB) j .. (64 / RB) (j + 1) - 1
+    const float tot = transposed_sum<RB>(part, lane);
+    // the slice partials meet in LDS; row t is summed (slices in order) and
+    // stored by lane t of wave 0
+    float* const kp = reinterpret_cast<float*>(smem + KS * wave_lds<ND>());
+    if ((lane & (64 / RB - 1)) == 0) kp[ws * RB + lane / (64 / RB)] = tot;
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (!t_mine) return;
+    float v = 0.f;
+    for (int w = 0; w < KS; ++w) v += kp[w * RB + t_row];
+    const auto yr = make_rsrc((char*)P.y + (size_t)r0 * ysz, (uint32_t)nrows * ysz);
+    const uint32_t yoff = (uint32_t)t_row * ysz;
+    if constexpr (YF32) {
+        if constexpr (BIAS) v += __uint_as_float(bias_bits);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yr, yoff, 0, QMVS_STORE_POLICY);
+    } else {
+        // rounded to y's dtype, then the bias added and rounded again (two MLX ops)
+        uint16_t h;
+        if (P.y_dtype == DT_F16) {
+            h = f32_to_f16_bits(f32_pinned(v));
+            if constexpr (BIAS) h = f32_to_f16_bits(f32_pinned(f16_bits_to_f32(h) + f16_bits_to_f32(bias_bits)));
+        } else {
+            h = f32_to_bf16_bits(v);
+            if constexpr (BIAS) h = f32_to_bf16_bits(bf16_bits_to_f32(h) + bf16_bits_to_f32(bias_bits));
+        }
+        __builtin_amdgcn_raw_buffer_store_b16(h, yr, yoff, 0, QMVS_STORE_POLICY);
+    }
+}
+
+// waves (K-slices) per block
+int slices(int64_t K, int bits) {
+    const int64_t slice_codes = (int64_t)kSliceBytes * 8 / bits;
+    return (int)((K + slice_codes - 1) / slice_codes);
+}
+
+// rows per block: 16 when that still gives the chip about 6 waves per CU
+// (fewer, longer waves: x is loaded once per 16 rows), else 8, else 4
+#ifndef QMVS_RB_FORCE
+#define QMVS_RB_FORCE 0
+#endif
+int rows_per_block(int64_t N, int ks) {
+    if (QMVS_RB_FORCE) return QMVS_RB_FORCE == 32 && ks > 7 ? 16 : QMVS_RB_FORCE;
+    const int64_t waves_wanted = (int64_t)num_cus() * 6;
+    if ((N + 15) / 16 * ks >= waves_wanted) return 16;
+    if ((N + 7) / 8 * ks >= waves_wanted / 2) return 8;
+    return 4;
+}
+
+template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS>
+hipError_t launch_t(const QmmArgs& a, int ks) {
+    const QmvsArgs P{(const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y, a.bias,
+                     (int)a.N, (int)a.K, __builtin_ctz((unsigned)a.group_size), a.y_dtype};
+    const size_t lds = (size_t)ks * wave_lds<ND>() + (size_t)ks * RB * 4;
+    const int blocks = (int)((a.N + RB - 1) / RB);
+    hipLaunchKernelGGL((qmvs_kernel<BITS, SBT, RB, ND, YF32, BIAS>), dim3(blocks), dim3(64 * ks), lds, a.stream, P);
+    return hipGetLastError();
+}
+
+template <int BITS, int SBT, int RB, bool YF32, bool BIAS>
+hipError_t launch_nd(const QmmArgs& a, int ks) {
+    // bytes of scales per row and slice: (1 KiB of codes / group) * 2
+    const int sb = 2 * ((kSliceBytes * 8 / BITS) / a.group_size);
+    if (RB * sb > 2 * kSliceBytes) return launch_t<BITS, SBT, RB, 4, YF32, BIAS>(a, ks);
+    if (RB * sb > kSliceBytes) return launch_t<BITS, SBT, RB, 2, YF32, BIAS>(a, ks);
+    return launch_t<BITS, SBT, RB, 1, YF32, BIAS>(a, ks);
+}
+
+template <int BITS, int SBT, bool YF32, bool BIAS>
+hipError_t launch_rb(const QmmArgs& a) {
+    const int ks = slices(a.K, BITS);
+    switch (rows_per_block(a.N, ks)) {
+        case 32: return launch_nd<BITS, SBT, 32, YF32, BIAS>(a, ks);
+        case 16: return launch_nd<BITS, SBT, 16, YF32, BIAS>(a, ks);
+        case 8: return launch_nd<BITS, SBT, 8, YF32, BIAS>(a, ks);
+        default: return launch_nd<BITS, SBT, 4, YF32, BIAS>(a, ks);
+    }
+}
+
+template <bool YF32, bool BIAS>
+hipError_t launch_y(const QmmArgs& a) {
+    if (a.bits == 4)
+        return a.sb_dtype == DT_F16 ? launch_rb<4, DT_F16, YF32, BIAS>(a) : launch_rb<4, DT_BF16, YF32, BIAS>(a);
+    return a.sb_dtype == DT_F16 ? launch_rb<8, DT_F16, YF32, BIAS>(a) : launch_rb<8, DT_BF16, YF32, BIAS>(a);
+}
+
+}  // namespace
+
+bool qmvs_supported(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
+    (void)N;
+    // up to 15 waves per block (LDS within the default 64 KiB); an even
+    // number of groups per row keeps the scale rows 4-byte aligned for the
+    // 16-byte direct-to-LDS loads
+    const int ks = slices(K, bits);
+    return M == 1 && ks >= 1 && ks <= 15 && (K / group_size) % 2 == 0;
+}
+
+void qmvs_config(const QmmArgs& a, int* rows_per_blk, int* slices_out, int* blocks) {
+    const int ks = slices(a.K, a.bits), rb = rows_per_block(a.N, ks);
+    if (rows_per_blk) *rows_per_blk = rb;
+    if (slices_out) *slices_out = ks;
+    if (blocks) *blocks = (int)((a.N + rb - 1) / rb);
+}
+
+hipError_t launch_qmvs(const QmmArgs& a) {
+    if (a.M != 1) return hipErrorInvalidValue;
+    if (a.y_dtype == DT_F32) return a.bias ? launch_y<true, true>(a) : launch_y<true, false>(a);
+    return a.bias ? launch_y<false, true>(a) : launch_y<false, false>(a);
+}
+
+}  // namespace miqmm

@@ -35,14 +35,16 @@ import torch
 __all__ = [
     "MiqmmError", "quantized_matmul", "quantized_linear", "QuantizedLinear", "dequantize",
     "unpack", "synth_problem", "query_route", "result_type", "lib", "LIB_PATH", "quantized_matmul_grouped",
+    "workspace_size",
     "Problem", "gather_qmm", "quantized_embedding", "QuantizedEmbedding",
     "OK", "EINVAL", "ENOTSUP", "EHIP", "ROUTE_AUTO", "ROUTE_QMV", "ROUTE_QMM", "ROUTE_QMV_DOT", "ROUTE_QMVX",
+    "ROUTE_QMVS",
 ]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmiqmm.so")
 
 OK, EINVAL, ENOTSUP, EHIP = 0, 1, 2, 3
-ROUTE_AUTO, ROUTE_QMV, ROUTE_QMM, ROUTE_QMV_DOT, ROUTE_QMVX = 0, 1, 2, 3, 4
+ROUTE_AUTO, ROUTE_QMV, ROUTE_QMM, ROUTE_QMV_DOT, ROUTE_QMVX, ROUTE_QMVS = 0, 1, 2, 3, 4, 5
 DT_BF16, DT_F16, DT_F32 = 0, 1, 2
 
 _DT = {torch.bfloat16: DT_BF16, torch.float16: DT_F16, torch.float32: DT_F32}
@@ -86,11 +88,14 @@ def lib() -> ctypes.CDLL:
     L.miqmm_gather_qmm.argtypes = [P, P, P, P, P, P, I64, I64, I, I64, I64, I64, I64, I, I, I, I, I, I, I, P]
     L.miqmm_quantized_embedding.argtypes = [P, P, I64, P, P, P, I64, I64, I, I, I, I, P]
     L.miqmm_gather_qmm_workspace_size.argtypes = [I64, I64, I64, ctypes.POINTER(I64)]
+    L.miqmm_quantized_matmul_workspace_size.argtypes = [I64, I64, I64, I, I, ctypes.POINTER(I64)]
+    L.miqmm_quantized_matmul_ws.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I, I, I, P, I64, P]
     L.miqmm_gather_qmm_ws.argtypes = [P, P, P, P, P, P, I64, I64, I, I64, I64, I64, I64, I, I, I, I, I, I, I, P,
                                       I64, P]
     for name in ("miqmm_quantized_matmul", "miqmm_quantized_matmul_ex", "miqmm_quantized_linear",
                  "miqmm_dequantize", "miqmm_unpack", "miqmm_query_route", "miqmm_synth_problem",
-                 "miqmm_quantized_matmul_grouped"):
+                 "miqmm_quantized_matmul_grouped", "miqmm_quantized_matmul_workspace_size",
+                 "miqmm_quantized_matmul_ws"):
         getattr(L, name).restype = I
     L.miqmm_last_error.argtypes, L.miqmm_last_error.restype = [], ctypes.c_char_p
     L.miqmm_version.argtypes, L.miqmm_version.restype = [], ctypes.c_char_p
@@ -169,14 +174,31 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
     if bias is not None:
         if bias.shape != (N,) or bias.dtype != out.dtype:
             raise MiqmmError(EINVAL, f"bias must be [{N}] of dtype {out.dtype}")
-        _check(lib().miqmm_quantized_linear(_ptr(out), _ptr(xc), _ptr(w), _ptr(scales), _ptr(biases),
-                                            _ptr(bias.contiguous()), M, N, K, group_size, bits, _dt(xc),
-                                            _dt(scales), _dt(out), _stream(stream)))
+        bias = bias.contiguous()
+        if route != ROUTE_AUTO and route != query_route(M, N, K, group_size, bits)[0]:
+            raise MiqmmError(EINVAL, "a bias takes the automatic route (a forced route only where it is that one)")
+        route = ROUTE_AUTO
+    if route == ROUTE_AUTO:
+        # the tiled matmul's k split needs scratch for its fp32 partials: taken
+        # from torch's caching allocator per call (stream-ordered, and from the
+        # graph's own pool under capture), so calls never share it
+        ws = workspace_size(M, N, K, group_size, bits)
+        wt = torch.empty(ws, dtype=torch.uint8, device=x.device) if ws > 0 else None
+        _check(lib().miqmm_quantized_matmul_ws(_ptr(out), _ptr(xc), _ptr(w), _ptr(scales), _ptr(biases),
+                                               _ptr(bias), M, N, K, int(bool(transpose)), group_size, bits,
+                                               _dt(xc), _dt(scales), _dt(out), _ptr(wt), ws, _stream(stream)))
         return out
     _check(lib().miqmm_quantized_matmul_ex(_ptr(out), _ptr(xc), _ptr(w), _ptr(scales), _ptr(biases), M, N,
                                            K, int(bool(transpose)), group_size, bits, _dt(xc), _dt(scales),
                                            _dt(out), route, _stream(stream)))
     return out
+
+
+def workspace_size(M: int, N: int, K: int, group_size: int = 64, bits: int = 4) -> int:
+    """bytes of scratch the automatic route's k split takes for this shape (0: none)"""
+    n = ctypes.c_int64(0)
+    _check(lib().miqmm_quantized_matmul_workspace_size(M, N, K, group_size, bits, ctypes.byref(n)))
+    return n.value
 
 
 def quantized_matmul_grouped(xs, ws, scales, biases, group_size: int = 64, bits: int = 4, *,

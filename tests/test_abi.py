@@ -61,6 +61,10 @@ def _qmm(lib, **kw):
     (dict(sd=2), 2, "scales/biases dtype"),
     (dict(yd=7), 1, "y dtype"),
     (dict(route=9), 1, "route"),
+    (dict(route=5, M=2), 2, "qmvs takes one row"),
+    (dict(route=5, K=32768, g=64), 2, "15 KiB"),
+    (dict(route=5, K=192, g=64), 2, "even K/group_size"),
+    (dict(route=5, s=ctypes.c_void_p(18)), 2, "4-byte aligned"),
     (dict(x=ctypes.c_void_p(8)), 1, "16-byte aligned"),
     (dict(w=ctypes.c_void_p(20)), 1, "16-byte aligned"),
     (dict(y=None), 1, "null pointer"),
@@ -174,17 +178,48 @@ def test_gather_python_shape_checks(lib):
         miqmm.gather_qmm(x, w, s, s, idx.float())
 
 
+def test_workspace_entry_points_validate(lib):
+    import miqmm
+
+    n = ctypes.c_int64(-1)
+    # GEMV routes and unsplit plans take no workspace; a split plan k ranges * M * N * 4
+    assert lib.miqmm_quantized_matmul_workspace_size(1, 4096, 4096, 64, 4, ctypes.byref(n)) == 0 and n.value == 0
+    assert lib.miqmm_quantized_matmul_workspace_size(2048, 14336, 4096, 64, 4, ctypes.byref(n)) == 0
+    assert n.value == 0
+    assert lib.miqmm_quantized_matmul_workspace_size(256, 4096, 4096, 64, 4, ctypes.byref(n)) == 0
+    ks = miqmm.query_route(256, 4096, 4096, 64, 4)[1][3]
+    assert ks > 1 and n.value == ks * 256 * 4096 * 4
+    assert miqmm.workspace_size(256, 4096, 4096) == n.value
+    assert lib.miqmm_quantized_matmul_workspace_size(0, 4096, 4096, 64, 4, ctypes.byref(n)) == 0 and n.value == 0
+    assert lib.miqmm_quantized_matmul_workspace_size(1, 4096, 4096, 64, 4, None) == 1
+    assert lib.miqmm_quantized_matmul_workspace_size(-1, 4096, 4096, 64, 4, ctypes.byref(n)) == 1
+    assert lib.miqmm_quantized_matmul_workspace_size(1, 4096, 4096, 48, 4, ctypes.byref(n)) == 1
+    P = ctypes.c_void_p
+    ws = lambda **kw: lib.miqmm_quantized_matmul_ws(
+        P(16), P(16), P(16), P(16), P(16), None, kw.get("M", 256), 4096, 4096, kw.get("transpose", 1), 64, 4, 0,
+        0, 0, kw.get("work", P(256)), kw.get("nbytes", 1 << 20), None)
+    assert ws(nbytes=-1) == 1 and "workspace_bytes" in lib.miqmm_last_error().decode()
+    assert ws(work=P(8)) == 1 and "16-byte aligned" in lib.miqmm_last_error().decode()
+    assert ws(transpose=0) == 2 and "transpose" in lib.miqmm_last_error().decode()
+    assert ws(M=0) == 0  # M == 0: nothing to do, nothing touched
+
+
 def test_query_route(lib):
     import miqmm
 
-    route, tiles = miqmm.query_route(1, 14336, 4096, 64, 4)
-    assert route == miqmm.ROUTE_QMV_DOT and tiles[0] in (1, 2, 4) and tiles[1] >= 1 and tiles[2] in (16, 32, 64)
-    assert miqmm.query_route(1, 4864, 896, 64, 4)[1][2] == 32  # 28 chunks per row -> 32 lanes
-    # rows per sub-group at M = 1: two from the x table on, four for rows of
-    # 8192 codes or more while four still give 1536 row tiles
-    assert miqmm.query_route(1, 14336, 4096, 64, 4)[1][0] == 2
-    assert miqmm.query_route(1, 8192, 28672, 64, 4)[1][0] == 4
-    assert miqmm.query_route(1, 4096, 14336, 64, 4)[1][0] == 2
+    # M = 1 with rows of 2048 codes or more: the K-sliced GEMV, one wave per
+    # 1 KiB slice of a row, 16 rows per block while that gives ~6 waves per CU
+    # (the CU count is 256 without a device)
+    assert miqmm.query_route(1, 14336, 4096, 64, 4) == (miqmm.ROUTE_QMVS, (16, 2, 896, 0))
+    assert miqmm.query_route(1, 4096, 14336, 64, 4) == (miqmm.ROUTE_QMVS, (16, 7, 256, 0))
+    assert miqmm.query_route(1, 6144, 4096, 64, 4) == (miqmm.ROUTE_QMVS, (8, 2, 768, 0))
+    assert miqmm.query_route(1, 262144, 5376, 32, 4) == (miqmm.ROUTE_QMVS, (16, 3, 16384, 0))
+    assert miqmm.query_route(1, 262144, 5376, 64, 8) == (miqmm.ROUTE_QMVS, (16, 6, 16384, 0))
+    # an odd number of groups per row keeps the v_dot2 GEMV (scale rows not 4-byte aligned)
+    assert miqmm.query_route(1, 4096, 2080, 32, 4)[0] == miqmm.ROUTE_QMV_DOT
+    # shorter rows: the v_dot2 GEMV, lanes per row by chunk count
+    route, tiles = miqmm.query_route(1, 4864, 896, 64, 4)
+    assert route == miqmm.ROUTE_QMV_DOT and tiles[2] == 32  # 28 chunks per row -> 32 lanes
     # wide, short-K head at M = 1 and 2 <= M <= 4: the LDS-staged MFMA GEMV (m tile, k-splits, codes per stage)
     route, tiles = miqmm.query_route(1, 151936, 896, 64, 4)
     assert route == miqmm.ROUTE_QMVX and tiles[:3] == (1, 1, 1024)
