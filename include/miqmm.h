@@ -27,7 +27,8 @@
  * asynchronous on `stream` (a hipStream_t; NULL = the default stream) and may
  * be captured into a HIP graph.  Every function returns a miqmm_status; on
  * failure miqmm_last_error() returns a message for the calling thread.
- * Calls are safe from several threads on distinct streams.
+ * Calls are safe from several threads on distinct streams, except
+ * miqmm_quantized_matmul_noalloc (see there).
  */
 #ifndef MIQMM_H
 #define MIQMM_H
@@ -149,6 +150,24 @@ int miqmm_quantized_matmul_ws(void* y, const void* x, const uint32_t* w, const v
                               const void* biases, const void* bias, int64_t M, int64_t N, int64_t K,
                               int transpose, int group_size, int bits, int x_dtype, int sb_dtype,
                               int y_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * miqmm_quantized_matmul_ws with the library's own scratch in place of a
+ * workspace argument: allocates nothing (no hipMalloc, no allocating library
+ * call), for callers that cannot allocate -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid it.  The scratch is a 32 MiB
+ * device array the code object holds on every GPU the library runs on (kept
+ * until the process ends); a shape whose k split needs more
+ * (miqmm_quantized_matmul_workspace_size > 32 MiB) returns MIQMM_EINVAL
+ * instead.  Every call on a GPU shares that GPU's array: calls that may
+ * overlap on one GPU (several streams, threads or graph replays in flight at
+ * once) race on it and must be serialized by the caller.  No counterpart in
+ * the reference.
+ */
+int miqmm_quantized_matmul_noalloc(void* y, const void* x, const uint32_t* w, const void* scales,
+                                   const void* biases, const void* bias, int64_t M, int64_t N, int64_t K,
+                                   int transpose, int group_size, int bits, int x_dtype, int sb_dtype,
+                                   int y_dtype, void* stream);
 
 /*
  * QuantizedLinear forward: y = quantized_matmul(...) rounded to y_dtype, then

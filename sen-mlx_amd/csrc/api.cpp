@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/miqmm.h"
@@ -257,6 +258,33 @@ int gather_common(void* y, const void* x, const uint32_t* w, const void* scales,
     return ok();
 }
 
+// Scratch of miqmm_quantized_matmul_noalloc: the tiled matmul's k-split
+// partials, in device memory the code object holds (each GPU the library
+// runs on has its own copy, kept until the process ends).  Its address on a
+// device comes from hipGetSymbolAddress, once per device, with the device
+// current; host code uses only that address.
+constexpr int64_t kNoallocScratchBytes = (int64_t)32 << 20;
+static __device__ __align__(256) char scratch[kNoallocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];  // per device id, set once under g_scratch_mu
+
+int scratch_address(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(MIQMM_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= 64) return fail(MIQMM_EINVAL, "device id %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return fail(MIQMM_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MIQMM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -383,6 +411,29 @@ int miqmm_gather_qmm_ws(void* y, const void* x, const uint32_t* w, const void* s
     return gather_common(y, x, w, scales, biases, rhs_indices, batch, top_k, x_per_index, M, N, K, experts, transpose,
                          group_size, bits, x_dtype, sb_dtype, y_dtype, sorted_indices, workspace, workspace_bytes,
                          stream);
+}
+
+int miqmm_quantized_matmul_noalloc(void* y, const void* x, const uint32_t* w, const void* scales,
+                                   const void* biases, const void* bias, int64_t M, int64_t N, int64_t K,
+                                   int transpose, int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
+                                   void* stream) {
+    bool noop;
+    int st = check_args(y, x, w, scales, biases, M, N, K, transpose, group_size, bits, x_dtype, sb_dtype, y_dtype,
+                        MIQMM_ROUTE_AUTO, &noop);
+    if (st != MIQMM_OK || noop) return st;
+    const int64_t need = split_workspace_bytes(M, N, K, group_size, bits);
+    if (need > kNoallocScratchBytes)
+        return fail(MIQMM_EINVAL,
+                    "M=%lld N=%lld K=%lld needs %lld bytes of k-split scratch, more than the %lld this entry "
+                    "point holds; use miqmm_quantized_matmul_ws",
+                    (long long)M, (long long)N, (long long)K, (long long)need, (long long)kNoallocScratchBytes);
+    void* ptr = nullptr;
+    if (need > 0) {
+        st = scratch_address(&ptr);
+        if (st != MIQMM_OK) return st;
+    }
+    return qmm_common(y, x, w, scales, biases, bias, M, N, K, transpose, group_size, bits, x_dtype, sb_dtype,
+                      y_dtype, MIQMM_ROUTE_AUTO, stream, ptr, need > 0 ? kNoallocScratchBytes : 0);
 }
 
 int miqmm_dequantize(void* out, const uint32_t* w, const void* scales, const void* biases,

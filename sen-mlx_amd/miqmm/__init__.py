@@ -90,12 +90,13 @@ def lib() -> ctypes.CDLL:
     L.miqmm_gather_qmm_workspace_size.argtypes = [I64, I64, I64, ctypes.POINTER(I64)]
     L.miqmm_quantized_matmul_workspace_size.argtypes = [I64, I64, I64, I, I, ctypes.POINTER(I64)]
     L.miqmm_quantized_matmul_ws.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I, I, I, P, I64, P]
+    L.miqmm_quantized_matmul_noalloc.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I, I, I, P]
     L.miqmm_gather_qmm_ws.argtypes = [P, P, P, P, P, P, I64, I64, I, I64, I64, I64, I64, I, I, I, I, I, I, I, P,
                                       I64, P]
     for name in ("miqmm_quantized_matmul", "miqmm_quantized_matmul_ex", "miqmm_quantized_linear",
                  "miqmm_dequantize", "miqmm_unpack", "miqmm_query_route", "miqmm_synth_problem",
                  "miqmm_quantized_matmul_grouped", "miqmm_quantized_matmul_workspace_size",
-                 "miqmm_quantized_matmul_ws"):
+                 "miqmm_quantized_matmul_ws", "miqmm_quantized_matmul_noalloc"):
         getattr(L, name).restype = I
     L.miqmm_last_error.argtypes, L.miqmm_last_error.restype = [], ctypes.c_char_p
     L.miqmm_version.argtypes, L.miqmm_version.restype = [], ctypes.c_char_p
