@@ -57,6 +57,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
 constexpr int64_t kMaxDim = (int64_t)1 << 31;
+// The kernels address a tile's rows of x, codes and scales through 32-bit
+// buffer offsets (256 rows of x take 512 K bytes): K up to 2^22 keeps every
+// such range below 2^31 bytes.
+constexpr int64_t kMaxK = (int64_t)1 << 22;
 // selections per expert (on average) from which gather_qmm groups them by
 // expert into the tiled matmul, when given a workspace
 #ifndef MIQMM_GROUPED_MIN
@@ -82,6 +86,9 @@ int check_quant(int64_t N, int64_t K, int group_size, int bits, int sb_dtype) {
         return fail(MIQMM_EINVAL, "group_size must be 32, 64 or 128, got %d", group_size);
     if (N <= 0 || K <= 0 || N >= kMaxDim || K >= kMaxDim)
         return fail(MIQMM_EINVAL, "N and K must be in [1, 2^31), got N=%lld K=%lld", (long long)N, (long long)K);
+    if (K > kMaxK)
+        return fail(MIQMM_EINVAL, "K=%lld exceeds %lld (the kernels' 32-bit tile offsets)", (long long)K,
+                    (long long)kMaxK);
     if (K % group_size != 0)
         return fail(MIQMM_EINVAL, "K=%lld is not a multiple of group_size=%d", (long long)K, group_size);
     if (sb_dtype != MIQMM_DT_BF16 && sb_dtype != MIQMM_DT_F16)

@@ -27,6 +27,7 @@
 #include <map>
 #include <memory>
 #include <set>
+#include <cstdint>
 #include <string>
 #include <vector>
 
@@ -335,7 +336,9 @@ int parse_shard(const std::string& path, std::vector<Tensor>& out) {
             if (!d.is_int() || d.num < 0)
                 return ckpt_fail(MIQMM_EINVAL, "%s: tensor %s has a bad shape", path.c_str(), kv.first.c_str());
             x.shape.push_back((int64_t)d.num);
-            count *= (int64_t)d.num;
+            // a product past INT64_MAX / 8 would wrap and could match the byte range by accident
+            if (__builtin_mul_overflow(count, (int64_t)d.num, &count) || count > INT64_MAX / 8)
+                return ckpt_fail(MIQMM_EINVAL, "%s: tensor %s has a shape too large", path.c_str(), kv.first.c_str());
         }
         const int64_t b = (int64_t)off->arr[0].num, e = (int64_t)off->arr[1].num;
         const int64_t es = dtype_size(x.dtype);

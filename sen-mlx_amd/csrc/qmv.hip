@@ -39,7 +39,6 @@ namespace {
 // per-selection tiles: 16 tokens of DeepSeek-V2-Lite 39.5 us at 8, 42.5 at 4)
 constexpr int kMaxBlocksPerCU = 4;
 constexpr int kMaxGatherBlocksPerCU = 8;
-constexpr int kNumCUs = 256;
 constexpr int64_t kFillTiles = 1536;  // row tiles that keep the chip busy (see pick_r)
 
 // one pipeline stage: the codes, scales and biases of R rows at one chunk
@@ -409,7 +408,7 @@ int use_ksplit(int64_t tiles, int64_t K, int bits, int L) {
 // per_cu blocks per CU, the waves then walking further tiles
 int gemv_blocks(int64_t tiles, int ksplit, int per_cu = kMaxBlocksPerCU) {
     const int64_t want = ksplit ? tiles : (tiles + 3) / 4;
-    return (int)(want < (int64_t)kNumCUs * per_cu ? want : (int64_t)kNumCUs * per_cu);
+    return (int)(want < (int64_t)num_cus() * per_cu ? want : (int64_t)num_cus() * per_cu);
 }
 
 // a[0..count) share M, K, group size, bits and dtypes; one grid covers all

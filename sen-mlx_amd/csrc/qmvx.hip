@@ -45,7 +45,6 @@ namespace {
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kMaxXElems = 32768;  // MT * K bf16 of x held in LDS (64 KiB)
-constexpr int kNumCUs = 256;
 
 // s_waitcnt immediate for vmcnt(n) lgkmcnt(0) (vmcnt bits 3:0 and 15:14, expcnt 6:4 left at 7)
 constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
@@ -401,7 +400,7 @@ hipError_t launch_t(const QmmArgs& a, int KS) {
     } else {
         // persistent waves: as many blocks as fit on the chip at once
         const int per_cu = (int)((160 * 1024) / L.total);
-        const int64_t cap = (int64_t)kNumCUs * (per_cu < 1 ? 1 : per_cu > 4 ? 4 : per_cu);
+        const int64_t cap = (int64_t)num_cus() * (per_cu < 1 ? 1 : per_cu > 4 ? 4 : per_cu);
         const int64_t want = (tiles + 3) / 4;
         blocks = (int)(want < cap ? want : cap);
     }

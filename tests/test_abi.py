@@ -56,6 +56,7 @@ def _qmm(lib, **kw):
     (dict(K=96, g=64), 1, "not a multiple of group_size"),
     (dict(N=0), 1, "N and K"),
     (dict(K=-64), 1, "N and K"),
+    (dict(K=(1 << 22) + 64), 1, "32-bit tile offsets"),
     (dict(M=-1), 1, "M must be"),
     (dict(xd=1), 2, "x dtype"),
     (dict(sd=2), 2, "scales/biases dtype"),

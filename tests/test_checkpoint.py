@@ -154,3 +154,23 @@ def test_malformed_shards(tmp_path):
     open(os.path.join(d, "config.json"), "w").write("{not json")
     with pytest.raises(miqmm.MiqmmError, match="config.json"):
         Checkpoint(d)
+
+
+def test_overflowing_shape_is_refused(tmp_path):
+    """a shard whose shape product overflows int64 (2^32 x 2^32 wraps to 0)
+    must not pass the byte-range check with an empty range"""
+    import json
+    import struct
+
+    import miqmm
+    from miqmm.checkpoint import Checkpoint
+
+    d = str(tmp_path)
+    make_model(d, QUANT, shards=1)
+    p = os.path.join(d, "model.safetensors")
+    hdr = {"model.norm.weight": {"dtype": "BF16", "shape": [1 << 32, 1 << 32], "data_offsets": [0, 0]}}
+    h = json.dumps(hdr).encode()
+    h += b" " * (-len(h) % 8)
+    open(p, "wb").write(struct.pack("<Q", len(h)) + h)
+    with pytest.raises(miqmm.MiqmmError, match="too large"):
+        Checkpoint(d)
