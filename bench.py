@@ -1,29 +1,39 @@
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-headline]
+    python bench.py --profile-target {step,qkv,o,gateup,down,lm_head,qmv,qmv_down,config0,qmm,read33,read77,copy}
 
-Workload (one "step"): the linear layers of one Qwen2.5-0.5B decode step at
-M=1, 4-bit group-64 affine weights with bf16 scales/biases:
-24 layers x {q 896->896, k 896->128, v 896->128, o 896->896, gate 896->4864,
-up 896->4864, down 4864->896} + lm_head 896->151936.  Weights are random
-(seeded, generated on the device); x ~ N(0,1) is drawn per layer input, as in
-the model: q, k and v read the attention input, gate and up the MLP input,
-o and down their own.  The step runs q/k/v and gate/up as one grouped call
-each (miqmm_quantized_matmul_grouped), 97 launches; the same step with one
-launch per projection (169 launches) is reported beside it.  The launches of
-a step are captured once per weight replica into a HIP graph and replayed;
-three replicas (838 MB) rotate so consecutive steps never find their weights
-in the 256 MB Infinity Cache.
+Workload (one "step", the line's `value`): the linear layers of one
+Qwen2.5-0.5B decode step at M=1, 4-bit group-64 affine weights with bf16
+scales/biases: 24 layers x {q 896->896, k 896->128, v 896->128, o 896->896,
+gate 896->4864, up 896->4864, down 4864->896} + lm_head 896->151936.  Weights
+are random (seeded, generated on the device); x ~ N(0,1) is drawn per layer
+input, as in the model: q, k and v read the attention input, gate and up the
+MLP input, o and down their own.  q/k/v and gate/up run as one grouped call
+each: 97 launches per step, captured once per weight replica into a HIP
+graph; three replicas (838 MB) rotate so no step finds its weights in the
+256 MB Infinity Cache.  W untimed steps, then exactly K timed steps between
+two device synchronizations, with HIP events on the replay stream.
 
-Printed: one JSON line with the step throughput (value, GB/s), the roofline
-of the dominant kernel (the lm_head GEMV, 76.9 MB per launch), headline
-numbers (qmv 4096x14336 at M=1, qmm at M=2048) and the CPU baseline (the C
-oracle's fp32 path on the host cores, same step, one replica).
+Every kernel-level figure follows one protocol: the calls are captured into
+a HIP graph cycling through enough distinct weight replicas that the bytes
+read exceed 512 MB (so nothing is served from the Infinity Cache), the graph
+is replayed at least 20 times with events around each replay, and the
+median per-call time is reported.  `roofline` is the step's kernel with the
+most time per step, measured this way on the step's own shapes.
+
+Printed: one JSON line (stdout) with the step throughput, the roofline of the
+dominant kernel, the headline numbers (qmv at M=1 on 4096x14336 and
+14336x4096 beside a bare streaming read of the same bytes; qmm at M=2048 and
+at the reference's prefill chunk M=512; configuration 0), the small-M and
+large-vocab sweeps, the expert gather and embedding rows, and the CPU
+baseline (the C oracle's fp32 path on the host cores, same decode step).
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -34,11 +44,14 @@ sys.path.insert(0, os.path.join(ROOT, "sen-mlx_amd"))
 METRIC = "qmv GB/s (% of HBM peak) at M=1; qmm TFLOP/s at M=2048, 4-bit g64"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+COLD_BYTES = 600e6   # distinct bytes one timed graph cycles through (> 2 x the 256 MB Infinity Cache)
+REPS = 20            # timed graph replays per figure (median reported)
 
 QWEN05_LAYER = [("q", 896, 896), ("k", 128, 896), ("v", 128, 896), ("o", 896, 896),
                 ("gate", 4864, 896), ("up", 4864, 896), ("down", 896, 4864)]
 QWEN05_LAYERS = 24
 LM_HEAD = ("lm_head", 151936, 896)
+SHAPES_8B = [(6144, 4096), (4096, 4096), (14336, 4096), (4096, 14336)]  # (N, K)
 
 
 def qbytes(M, N, K, bits=4, g=64, sb=2, xb=2, yb=2):
@@ -49,6 +62,12 @@ def qbytes(M, N, K, bits=4, g=64, sb=2, xb=2, yb=2):
 def group_bytes(Ns, K, M=1):
     """a grouped call reads x once: the projections' bytes minus the repeated x"""
     return sum(qbytes(M, N, K) for N in Ns) - (len(Ns) - 1) * M * K * 2
+
+
+# the step's launch types: (name, output rows of each grouped projection, K, launches per step)
+STEP_TYPES = [("qkv", [896, 128, 128], 896, QWEN05_LAYERS), ("o", [896], 896, QWEN05_LAYERS),
+              ("gateup", [4864, 4864], 896, QWEN05_LAYERS), ("down", [896], 4864, QWEN05_LAYERS),
+              ("lm_head", [LM_HEAD[1]], LM_HEAD[2], 1)]
 
 
 def step_shapes():
@@ -80,10 +99,22 @@ def make_replica(miqmm, torch, replica, shapes):
     return projs
 
 
+def call(miqmm, p):
+    miqmm.quantized_matmul(p.x, p.w, p.s, p.b, True, 64, 4, out=p.y)
+
+
+def call_group(miqmm, grp):
+    if len(grp) == 1:
+        call(miqmm, grp[0])
+    else:
+        miqmm.quantized_matmul_grouped([p.x for p in grp], [p.w for p in grp], [p.s for p in grp],
+                                       [p.b for p in grp], 64, 4, outs=[p.y for p in grp])
+
+
 def run_step(miqmm, projs):
     """one launch per projection (169)"""
     for p in projs:
-        miqmm.quantized_matmul(p.x, p.w, p.s, p.b, True, 64, 4, out=p.y)
+        call(miqmm, p)
 
 
 def run_step_grouped(miqmm, projs):
@@ -91,14 +122,8 @@ def run_step_grouped(miqmm, projs):
     for layer in range(QWEN05_LAYERS):
         q, k, v, o, gate, up, down = projs[layer * 7:layer * 7 + 7]
         for grp in ((q, k, v), (o,), (gate, up), (down,)):
-            if len(grp) == 1:
-                p = grp[0]
-                miqmm.quantized_matmul(p.x, p.w, p.s, p.b, True, 64, 4, out=p.y)
-            else:
-                miqmm.quantized_matmul_grouped([p.x for p in grp], [p.w for p in grp], [p.s for p in grp],
-                                               [p.b for p in grp], 64, 4, outs=[p.y for p in grp])
-    p = projs[-1]
-    miqmm.quantized_matmul(p.x, p.w, p.s, p.b, True, 64, 4, out=p.y)
+            call_group(miqmm, grp)
+    call(miqmm, projs[-1])
 
 
 def step_bytes_grouped():
@@ -115,7 +140,7 @@ def capture(torch, fn):
 
 
 def time_graphs(torch, graphs, reps):
-    """events on the replay stream around `reps` replays; returns seconds"""
+    """events on the replay stream around `reps` replays (cycling `graphs`); seconds"""
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -128,75 +153,156 @@ def time_graphs(torch, graphs, reps):
     return start.elapsed_time(end) / 1e3
 
 
-def kernel_roofline(miqmm, torch, N, K, M, replicas, launches_per_graph, reps, g=64, bits=4, sb_dtype=None):
-    """average duration of back-to-back launches of one shape over rotating
-    weight replicas (cold in the Infinity Cache); returns (avg_s, bytes_per_launch)"""
+def graph_median(torch, fns, launches, reps=REPS):
+    """median over `reps` replays of the time per call, one graph of `launches`
+    calls cycling through `fns` (one per weight replica); seconds"""
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(launches):
+            fns[i % len(fns)]()
+    g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    times = []
+    for _ in range(reps):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        g.replay()
+        end.record(stream)
+        end.synchronize()
+        times.append(start.elapsed_time(end) / 1e3 / launches)
+    del g
+    times.sort()
+    return times[len(times) // 2]
+
+
+def replicas_for(nbytes, minimum=2):
+    return max(minimum, math.ceil(COLD_BYTES / nbytes))
+
+
+def gemv_line(miqmm, torch, M, N, K, g=64, bits=4, sb_dtype=None, reps=REPS):
+    """per-call median of one shape over cold rotating replicas: (seconds, algorithmic bytes)"""
     sb_dtype = sb_dtype or torch.bfloat16
     ydt = miqmm.result_type(torch.bfloat16, sb_dtype)
+    nb = qbytes(M, N, K, bits, g, yb=4 if ydt == torch.float32 else 2)
     sets = []
-    for r in range(replicas):
+    for r in range(replicas_for(nb)):
         x, w, s, b = miqmm.synth_problem(M, N, K, g, bits, sb_dtype=sb_dtype, seed=100 + r, stream_id=N + K)
         sets.append((x, w, s, b, torch.empty((M, N), dtype=ydt, device="cuda")))
-
-    def body():
-        for i in range(launches_per_graph):
-            x, w, s, b, y = sets[i % replicas]
-            miqmm.quantized_matmul(x, w, s, b, True, g, bits, out=y)
-
-    body()
-    torch.cuda.synchronize()
-    graph = capture(torch, body)
-    graph.replay()
-    t = time_graphs(torch, [graph], reps)
-    del sets
-    return t / (reps * launches_per_graph), qbytes(M, N, K, bits, g, yb=4 if ydt == torch.float32 else 2)
+    fns = [lambda t=t: miqmm.quantized_matmul(t[0], t[1], t[2], t[3], True, g, bits, out=t[4]) for t in sets]
+    sec = graph_median(torch, fns, max(len(fns), 40), reps)
+    del sets, fns
+    return sec, nb
 
 
-def qmm_tflops(miqmm, torch, M, N, K, iters):
-    x, w, s, b = miqmm.synth_problem(M, N, K, 64, 4, seed=7, stream_id=N + K)
-    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    for _ in range(2):
+def read_ceiling(miqmm, torch, nbytes, reps=REPS):
+    """a bare streaming read of nbytes (rounded up to 16 KiB) over cold rotating buffers"""
+    nb = (nbytes + 16383) // 16384 * 16384
+    bufs = [torch.full((nb,), r + 1, dtype=torch.uint8, device="cuda") for r in range(replicas_for(nb))]
+    sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    fns = [lambda b=b: miqmm.stream_read(b, sink) for b in bufs]
+    sec = graph_median(torch, fns, max(len(fns), 40), reps)
+    del bufs
+    return sec, nb
+
+
+def line(sec, nb):
+    gbs = nb / sec / 1e9
+    return {"us": round(sec * 1e6, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": nb}
+
+
+def step_type_line(miqmm, torch, Ns, K, reps=REPS):
+    """one of the step's launch types on its own: grouped projections (shared x)
+    or a single one, cold replicas; (seconds per launch, algorithmic bytes per launch)"""
+    nb = group_bytes(Ns, K) if len(Ns) > 1 else qbytes(1, Ns[0], K)
+    groups = []
+    for r in range(replicas_for(nb)):
+        x = None
+        grp = []
+        for j, N in enumerate(Ns):
+            p = Proj()
+            p.N, p.K = N, K
+            p.x, p.w, p.s, p.b = miqmm.synth_problem(1, N, K, 64, 4, seed=200 + r, stream_id=10 * j + N)
+            if x is None:
+                x = p.x
+            p.x = x
+            p.y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+            grp.append(p)
+        groups.append(grp)
+    fns = [lambda grp=grp: call_group(miqmm, grp) for grp in groups]
+    sec = graph_median(torch, fns, max(len(fns), 64), reps)
+    del groups, fns
+    return sec, nb
+
+
+def qmm_line(miqmm, torch, M, N, K, launches=50, reps=REPS, check=False):
+    """tiled matmul, graph-timed over `launches` calls (two weight replicas),
+    median of `reps` replays; optional elementwise check against a float32
+    reference (exactly dequantized W, float32 matmul)"""
+    sets = []
+    for r in range(2):
+        x, w, s, b = miqmm.synth_problem(M, N, K, 64, 4, seed=7 + r, stream_id=N + K)
+        sets.append((x, w, s, b, torch.empty((M, N), dtype=torch.bfloat16, device="cuda")))
+    fns = [lambda t=t: miqmm.quantized_matmul(t[0], t[1], t[2], t[3], True, 64, 4, out=t[4]) for t in sets]
+    sec = graph_median(torch, fns, launches, reps)
+    tf = 2.0 * M * N * K / sec / 1e12
+    out = {"TFLOP/s": round(tf, 1), "us": round(sec * 1e6, 2), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+           "route": miqmm.query_route(M, N, K, 64, 4)[1]}
+    if check:
+        x, w, s, b, y = sets[0]
         miqmm.quantized_matmul(x, w, s, b, True, 64, 4, out=y)
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(iters):
-        miqmm.quantized_matmul(x, w, s, b, True, 64, 4, out=y)
-    end.record()
-    torch.cuda.synchronize()
-    t = start.elapsed_time(end) / 1e3 / iters
-    return 2.0 * M * N * K / t / 1e12, t
+        wd = miqmm.dequantize(w, s, b, 64, 4, dtype=torch.float32)
+        prev = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = False
+        ref = x.float() @ wd.T
+        torch.backends.cuda.matmul.allow_tf32 = prev
+        err = (y.float() - ref).abs()
+        out["elem_ok_frac"] = round(((err <= 1e-3 + 1e-2 * ref.abs()).float().mean()).item(), 5)
+        out["max_err_over_max_ref"] = round((err.max() / ref.abs().max()).item(), 6)
+        del wd, ref, err
+    del sets, fns
+    return out
 
 
-def dense_bf16_tflops(torch, M, N, K, iters):
+def dense_bf16_tflops(torch, M, N, K, launches=50, reps=REPS):
     """hipBLASLt dense bf16 GEMM of the same shape (cross-check of the MFMA ceiling)"""
     a = torch.randn((M, K), dtype=torch.bfloat16, device="cuda")
     bt = torch.randn((N, K), dtype=torch.bfloat16, device="cuda")
-    for _ in range(2):
-        torch.matmul(a, bt.t())
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(iters):
-        torch.matmul(a, bt.t())
-    end.record()
-    torch.cuda.synchronize()
-    t = start.elapsed_time(end) / 1e3 / iters
-    return 2.0 * M * N * K / t / 1e12
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    sec = graph_median(torch, [lambda: torch.matmul(a, bt.t(), out=y)], launches, reps)
+    return round(2.0 * M * N * K / sec / 1e12, 1)
+
+
+def host_info():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "model": model,
+            "affinity": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
 
 
 def cpu_baseline(miqmm, torch, projs, budget_s=15.0):
     """the C oracle's fp32 path (OpenMP over N) on the host cores, on the same
-    decode step (one replica), repeated until ~budget_s of CPU time"""
+    decode step (one replica), repeated until ~budget_s of wall time"""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
     O.build_c_oracle()
-    threads = min(16, os.cpu_count() or 1)
+    info = host_info()
+    # the host's CPU share: OMP_NUM_THREADS when set (the GPU box sets it), else every core available
+    threads = int(os.environ.get("OMP_NUM_THREADS") or info["affinity"] or info["nproc"] or 1)
     host = []
     for p in projs:
         host.append((p.x.view(torch.int16).cpu().numpy().view(np.uint16),
@@ -216,46 +322,27 @@ def cpu_baseline(miqmm, torch, projs, budget_s=15.0):
     return {"value": round(step_bytes * steps / el / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"{steps} full decode steps (169 GEMVs, {step_bytes} B each) of one weight replica, "
-                      f"C oracle fp32 path (oracle/miqmm_oracle.c, gcc -O3 -fopenmp), {threads} threads, "
-                      f"{el:.1f} s; MLX's CPU backend is not available offline",
-            "ms_per_step": round(el / steps * 1e3, 3)}
-
-
-def graph_avg(torch, fns, launches, reps):
-    """average time of one call, over a HIP graph of `launches` calls cycling
-    through `fns` (one per weight replica, so the weights come cold from HBM)"""
-    for f in fns:
-        f()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for i in range(launches):
-            fns[i % len(fns)]()
-    g.replay()
-    torch.cuda.synchronize()
-    t = time_graphs(torch, [g], reps)
-    return t / (reps * launches)
+                      f"C oracle fp32 path (oracle/miqmm_oracle.c, gcc -O3 -fopenmp), {threads} threads "
+                      f"(host: {info['nproc']} logical CPUs, {info['affinity']} in this process's affinity, "
+                      f"{info['model']}), {el:.1f} s; MLX's CPU backend is not available offline",
+            "host": info, "ms_per_step": round(el / steps * 1e3, 3)}
 
 
 def small_m_and_large_vocab(miqmm, torch):
     """the GEMV routes beyond the decode step: speculative-verify / small-batch
     rows M in {1, 2, 4, 8, 16} on the Llama-3-8B projections (4-bit g64), and
     the Gemma-3-27B-class head K = 5376, N = 262144 at M in {1, 8} with fp16
-    scales, 4-bit g32 and 8-bit g64; weights cold (rotating replicas)"""
+    scales, 4-bit g32 and 8-bit g64; cold weights, median of 20 replays"""
     res = {}
-    for (N, K) in [(6144, 4096), (4096, 4096), (14336, 4096), (4096, 14336)]:
+    for (N, K) in SHAPES_8B:
         for M in (1, 2, 4, 8, 16):
-            avg, nb = kernel_roofline(miqmm, torch, N, K, M, replicas=10, launches_per_graph=40, reps=3)
-            res[f"qmv_m{M}_{K}to{N}"] = {"us": round(avg * 1e6, 2), "GB/s": round(nb / avg / 1e9, 1),
-                                         "frac_hbm": round(nb / avg / 1e9 / HBM_PEAK_GBS, 4)}
+            sec, nb = gemv_line(miqmm, torch, M, N, K)
+            res[f"qmv_m{M}_{K}to{N}"] = line(sec, nb)
         torch.cuda.empty_cache()
     for (bits, g) in [(4, 32), (8, 64)]:
         for M in (1, 8):
-            avg, nb = kernel_roofline(miqmm, torch, 262144, 5376, M, replicas=2, launches_per_graph=8, reps=3,
-                                      g=g, bits=bits, sb_dtype=torch.float16)
-            res[f"head_5376to262144_m{M}_{bits}bit_g{g}_f16"] = {
-                "us": round(avg * 1e6, 2), "GB/s": round(nb / avg / 1e9, 1),
-                "frac_hbm": round(nb / avg / 1e9 / HBM_PEAK_GBS, 4)}
+            sec, nb = gemv_line(miqmm, torch, M, 262144, 5376, g=g, bits=bits, sb_dtype=torch.float16)
+            res[f"head_5376to262144_m{M}_{bits}bit_g{g}_f16"] = line(sec, nb)
         torch.cuda.empty_cache()
     return res
 
@@ -279,10 +366,8 @@ def moe_and_embedding(miqmm, torch):
         yg = torch.empty(T, top_k, 1, I, device="cuda", dtype=torch.bfloat16)
         yd = torch.empty(T, top_k, 1, H, device="cuda", dtype=torch.bfloat16)
         n = 64 if T < 1024 else 16
-        tg = graph_avg(torch, [lambda s=s: miqmm.gather_qmm(x, *s[0], idx, True, g, 4, out=yg) for s in stacks],
-                       n, 5)
-        td = graph_avg(torch, [lambda s=s: miqmm.gather_qmm(h, *s[1], idx, True, g, 4, out=yd) for s in stacks],
-                       n, 5)
+        tg = graph_median(torch, [lambda s=s: miqmm.gather_qmm(x, *s[0], idx, True, g, 4, out=yg) for s in stacks], n)
+        td = graph_median(torch, [lambda s=s: miqmm.gather_qmm(h, *s[1], idx, True, g, 4, out=yd) for s in stacks], n)
         fl = 2 * T * top_k * H * I
         S = T * top_k
         path = ("expert-grouped tiled matmul" if S >= miqmm.GROUPED_MIN_PER_EXPERT * E else
@@ -301,46 +386,74 @@ def moe_and_embedding(miqmm, torch):
     for T in (1, 2048):
         ids = torch.randint(0, V, (T,), device="cuda", dtype=torch.int32)
         out = torch.empty(T, K, device="cuda", dtype=torch.bfloat16)
-        t = graph_avg(torch, [lambda tb=tb: miqmm.quantized_embedding(ids, *tb, g, 4, out=out) for tb in tabs], 64, 5)
+        t = graph_median(torch, [lambda tb=tb: miqmm.quantized_embedding(ids, *tb, g, 4, out=out) for tb in tabs], 64)
         nb = T * (K // 2 + 2 * (K // g) * 2 + K * 2)
         res[f"embedding_T{T}"] = {"us": round(t * 1e6, 2), "bytes": nb, "GB/s": round(nb / t / 1e9, 1)}
     return res
 
 
 PROFILE_DIR = os.path.join(ROOT, "profiles")
-ROOFLINE_PROFILE = os.path.join(PROFILE_DIR, "qmv_lm_head_151936x896_m1.md")
 
 
-def measured_traffic(path=ROOFLINE_PROFILE):
+def measured_traffic(kernel):
     """HBM bytes per launch of the roofline kernel from its committed rocprofv3
     summary (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), or None"""
+    path = os.path.join(PROFILE_DIR, f"step_{kernel}_m1.md")
     try:
         with open(path) as f:
-            for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":")[1])
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_launch:"):
+                    return int(ln.split(":")[1])
     except OSError:
         pass
     return None
 
 
+def step_types(miqmm, torch):
+    """each launch type of the step on its own (cold, median of 20 replays):
+    time per launch, bytes per launch, and time per step (launches x time)"""
+    res = {}
+    for name, Ns, K, count in STEP_TYPES:
+        sec, nb = step_type_line(miqmm, torch, Ns, K)
+        r = line(sec, nb)
+        r["launches_per_step"] = count
+        r["us_per_step"] = round(sec * 1e6 * count, 2)
+        r["route"] = miqmm.query_route(1, Ns[0], K, 64, 4)[0] if len(Ns) == 1 else "grouped v_dot2"
+        res[name] = r
+        torch.cuda.empty_cache()
+    return res
+
+
 def profile_section(miqmm, torch, target):
     """one measured section alone, so a rocprofv3 run of this command holds only
-    its kernel: the roofline launches, the qmv or qmm headline, or a plain
-    512 MiB device copy (the FETCH_SIZE / WRITE_SIZE calibration)"""
-    if target == "roofline":
-        avg, nb = kernel_roofline(miqmm, torch, LM_HEAD[1], LM_HEAD[2], 1, replicas=8,
-                                  launches_per_graph=64, reps=8)
-        return {"section": target, "shape": "M=1 N=151936 K=896", "timed_launches": 512,
-                "avg_launch_us": round(avg * 1e6, 3), "bytes_per_launch": nb, "GB/s": round(nb / avg / 1e9, 1)}
-    if target == "qmv":
-        avg, nb = kernel_roofline(miqmm, torch, 14336, 4096, 1, replicas=24, launches_per_graph=96, reps=6)
-        return {"section": target, "shape": "M=1 N=14336 K=4096", "timed_launches": 576,
-                "avg_launch_us": round(avg * 1e6, 3), "bytes_per_launch": nb, "GB/s": round(nb / avg / 1e9, 1)}
+    its kernels: a step launch type, the qmv / qmm headline shapes, config 0,
+    a bare streaming read, the decode step, or a plain 512 MiB device copy (the
+    FETCH_SIZE / WRITE_SIZE calibration)"""
+    types = {n: (Ns, K) for n, Ns, K, _ in STEP_TYPES}
+    if target in types:
+        Ns, K = types[target]
+        sec, nb = step_type_line(miqmm, torch, Ns, K)
+        return {"section": target, "shapes": [(N, K) for N in Ns], "replays": REPS,
+                **line(sec, nb)}
+    if target in ("qmv", "qmv_down", "config0"):
+        N, K = {"qmv": (14336, 4096), "qmv_down": (4096, 14336), "config0": (4864, 896)}[target]
+        sec, nb = gemv_line(miqmm, torch, 1, N, K)
+        return {"section": target, "shape": f"M=1 N={N} K={K}", "replays": REPS, **line(sec, nb)}
+    if target in ("read33", "read77"):
+        sec, nb = read_ceiling(miqmm, torch, 33067008 if target == "read33" else 76881408)
+        return {"section": target, "replays": REPS, **line(sec, nb)}
     if target == "qmm":
-        tf, tsec = qmm_tflops(miqmm, torch, 2048, 14336, 4096, iters=10)
-        return {"section": target, "shape": "M=2048 N=14336 K=4096", "timed_launches": 10,
-                "avg_launch_us": round(tsec * 1e6, 2), "TFLOP/s": round(tf, 1)}
+        return {"section": target, "shape": "M=2048 N=14336 K=4096", **qmm_line(miqmm, torch, 2048, 14336, 4096)}
+    if target == "step":
+        shapes = step_shapes()
+        replicas = [make_replica(miqmm, torch, r, shapes) for r in range(3)]
+        for projs in replicas:
+            run_step_grouped(miqmm, projs)
+        torch.cuda.synchronize()
+        graphs = [capture(torch, (lambda p=projs: run_step_grouped(miqmm, p))) for projs in replicas]
+        time_graphs(torch, graphs, 3)
+        t = time_graphs(torch, graphs, 30)
+        return {"section": target, "steps": 30, "us_per_step": round(t / 30 * 1e6, 2)}
     n = 512 << 20
     a = torch.empty(n // 4, dtype=torch.int32, device="cuda").fill_(1)
     b = torch.empty_like(a)
@@ -358,7 +471,9 @@ def main():
     ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-headline", action="store_true")
-    ap.add_argument("--profile-target", choices=["roofline", "qmv", "qmm", "copy"], default=None,
+    ap.add_argument("--profile-target", default=None,
+                    choices=["step", "qkv", "o", "gateup", "down", "lm_head", "qmv", "qmv_down", "config0", "qmm",
+                             "read33", "read77", "copy"],
                     help="run only this measured section and print its figures (for rocprofv3 summaries)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -399,11 +514,13 @@ def main():
     t1 = time_graphs(torch, graphs, args.steps)
     single = {"us_per_step": round(t1 / args.steps * 1e6, 2), "launches": len(shapes),
               "GB/s": round(step_bytes_single * args.steps / t1 / 1e9, 2), "bytes_per_step": step_bytes_single}
+    del graphs, replicas
+    torch.cuda.empty_cache()
 
-    # dominant kernel of the step: the lm_head GEMV (N=151936, K=896)
-    lm_avg, lm_bytes = kernel_roofline(miqmm, torch, LM_HEAD[1], LM_HEAD[2], 1, replicas=8,
-                                       launches_per_graph=64, reps=8)
-    lm_gbs = lm_bytes / lm_avg / 1e9
+    # the step's launch types on their own; the roofline kernel is the one with the most time per step
+    types = step_types(miqmm, torch)
+    dom = max(types, key=lambda k: types[k]["us_per_step"])
+    d = types[dom]
     out = {
         "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
@@ -415,35 +532,39 @@ def main():
                                "q/k/v and gate/up as one grouped call each",
                    "launches_per_step": 97, "bytes_per_step": step_bytes,
                    "weight_replicas": args.replicas, "hip_graph": True},
-        "roofline": {"kernel": "lm_head 896->151936 M=1 (qmvx_kernel<4, 0, 1, 6>: 4-bit, bf16 scales, 1 row of x, group 64)", "bound": "hbm",
-                     "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "avg_launch_us": round(lm_avg * 1e6, 3), "bytes_per_launch": lm_bytes},
+        "roofline": {"kernel": f"{dom}: the step's launch type with the most time per step "
+                               f"({d['launches_per_step']} launches x {d['us']} us = {d['us_per_step']} us of "
+                               f"{round(ms_per_step * 1e3, 1)} us; route {d['route']})",
+                     "bound": "hbm", "achieved": d["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": d["frac_hbm"], "traffic": measured_traffic(dom),
+                     "avg_launch_us": d["us"], "bytes_per_launch": d["bytes"]},
+        "step_types": types,
+        "step_one_launch_per_projection": single,
     }
-    out["step_one_launch_per_projection"] = single
     print(f"# step {ms_per_step * 1e3:.1f} us, {gbs:.1f} GB/s (one launch per projection: "
-          f"{single['us_per_step']:.1f} us); lm_head {lm_avg * 1e6:.2f} us {lm_gbs:.1f} GB/s",
-          file=sys.stderr, flush=True)
-    del graphs, replicas
+          f"{single['us_per_step']:.1f} us); types {json.dumps(types)}", file=sys.stderr, flush=True)
     torch.cuda.empty_cache()
 
     if not args.no_headline:
         head = {}
-        avg, nb = kernel_roofline(miqmm, torch, 14336, 4096, 1, replicas=24, launches_per_graph=96, reps=6)
-        head["qmv_m1_4096x14336"] = {"us": round(avg * 1e6, 3), "GB/s": round(nb / avg / 1e9, 1),
-                                     "frac_hbm": round(nb / avg / 1e9 / HBM_PEAK_GBS, 4), "bytes": nb}
-        print(f"# qmv 4096x14336 M=1: {avg * 1e6:.2f} us {nb / avg / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
-        avg, nb = kernel_roofline(miqmm, torch, 4096, 14336, 1, replicas=24, launches_per_graph=96, reps=6)
-        head["qmv_m1_14336x4096"] = {"us": round(avg * 1e6, 3), "GB/s": round(nb / avg / 1e9, 1),
-                                     "frac_hbm": round(nb / avg / 1e9 / HBM_PEAK_GBS, 4), "bytes": nb}
-        print(f"# qmv 14336x4096 M=1: {avg * 1e6:.2f} us {nb / avg / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
-        for (N, K) in [(14336, 4096), (4096, 14336), (6144, 4096), (4096, 4096)]:
-            tf, tsec = qmm_tflops(miqmm, torch, 2048, N, K, iters=10)
-            head[f"qmm_m2048_{K}to{N}"] = {"TFLOP/s": round(tf, 1), "us": round(tsec * 1e6, 1),
-                                           "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
-            print(f"# qmm M=2048 {K}->{N}: {tf:.1f} TFLOP/s ({tsec * 1e6:.1f} us)", file=sys.stderr, flush=True)
-        head["dense_bf16_gemm_m2048_4096to14336_torch"] = {
-            "TFLOP/s": round(dense_bf16_tflops(torch, 2048, 14336, 4096, 10), 1)}
+        for name, (N, K) in {"qmv_m1_4096x14336": (14336, 4096), "qmv_m1_14336x4096": (4096, 14336),
+                             "config0_qmv_m1_896x4864": (4864, 896)}.items():
+            sec, nb = gemv_line(miqmm, torch, 1, N, K)
+            head[name] = line(sec, nb)
+            head[name]["route"] = miqmm.query_route(1, N, K, 64, 4)[0]
+        for name, nbytes in {"bare_read_33MB": 33067008, "bare_read_77MB": 76881408}.items():
+            sec, nb = read_ceiling(miqmm, torch, nbytes)
+            head[name] = line(sec, nb)
+        print(f"# qmv / read: {json.dumps(head)}", file=sys.stderr, flush=True)
+        for M in (2048, 512):
+            for (N, K) in [(14336, 4096), (4096, 14336), (6144, 4096), (4096, 4096)]:
+                head[f"qmm_m{M}_{K}to{N}"] = qmm_line(miqmm, torch, M, N, K, check=(M == 2048))
+                print(f"# qmm M={M} {K}->{N}: {json.dumps(head[f'qmm_m{M}_{K}to{N}'])}", file=sys.stderr,
+                      flush=True)
+            torch.cuda.empty_cache()
+        head["qmm_m512_896to151936_lm_head"] = qmm_line(miqmm, torch, 512, 151936, 896)
+        head["dense_bf16_gemm_m2048_4096to14336_torch"] = {"TFLOP/s": dense_bf16_tflops(torch, 2048, 14336, 4096)}
+        head["dense_bf16_gemm_m512_4096to14336_torch"] = {"TFLOP/s": dense_bf16_tflops(torch, 512, 14336, 4096)}
         out["headline"] = head
         torch.cuda.empty_cache()
         out["small_m_and_large_vocab"] = small_m_and_large_vocab(miqmm, torch)

@@ -277,6 +277,15 @@ int miqmm_synth_problem(void* x, uint32_t* w, void* scales, void* biases, int64_
                         int64_t K, int group_size, int bits, int x_dtype, int sb_dtype,
                         uint64_t seed, uint64_t stream_id, void* stream);
 
+/*
+ * A plain streaming read of bytes (a multiple of 16384, below 2^31) from p
+ * (16-byte aligned): 16-byte non-temporal loads, 16 KiB per block, nothing
+ * written (sink: 4 KiB the kernel could write, never does in practice).
+ * No reference counterpart: the bandwidth ceiling the GEMVs are measured
+ * against in the benchmark.
+ */
+int miqmm_stream_read(const void* p, int64_t bytes, void* sink, void* stream);
+
 /* Message for the last failing call on this thread ("" if none). */
 const char* miqmm_last_error(void);
 

@@ -520,6 +520,14 @@ int miqmm_synth_problem(void* x, uint32_t* w, void* scales, void* biases, int64_
                         "synth launch");
 }
 
+int miqmm_stream_read(const void* p, int64_t bytes, void* sink, void* stream) {
+    if (!p || !sink) return fail(MIQMM_EINVAL, "null pointer argument");
+    if (!aligned16(p) || bytes <= 0 || bytes % 16384 != 0 || bytes >= ((int64_t)1 << 31))
+        return fail(MIQMM_EINVAL, "p must be 16-byte aligned and bytes a multiple of 16384 below 2^31");
+    return check_launch(miqmm::launch_stream_read(p, bytes, sink, reinterpret_cast<hipStream_t>(stream)),
+                        "stream read launch");
+}
+
 const char* miqmm_last_error(void) { return g_last_error.c_str(); }
 
 const char* miqmm_version(void) { return "miqmm 0.1.0 gfx950"; }

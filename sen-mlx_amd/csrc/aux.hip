@@ -11,6 +11,11 @@
 // the packed table, its scales and biases, then dequantize): out[t, k] =
 // fma(s, q, b) of row ids[t], in fp32, stored in the output dtype.
 //
+// stream_read: a plain streaming read of a buffer (each block 16 KiB, four
+// 16-byte loads per thread, non-temporal, the loaded words folded into one
+// value that is stored only if it equals a constant no buffer holds): the
+// bandwidth ceiling the GEMVs are measured against.
+//
 // synth: splitmix64 counter hash, draw i of stream (seed, tag) is
 // mix64(mix64(seed*G + tag) + i*G) with G = 0x9E3779B97F4A7C15; an
 // approximately N(0,1) value is the Irwin-Hall(4) sum of the draw's four
@@ -255,6 +260,26 @@ hipError_t launch_synth(void* x, uint32_t* w, void* scales, void* biases, int64_
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+namespace {
+__global__ __launch_bounds__(256) void stream_read_kernel(const char* __restrict__ p, uint32_t bytes,
+                                                          uint32_t* __restrict__ sink) {
+    const auto r = make_rsrc(p, bytes);
+    const uint32_t base = (blockIdx.x * 256u * 4u + threadIdx.x) * 16u;
+    u32x4_t acc = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc ^= bload16_nt(r, base + i * 4096u);
+    const uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+    if (v == 0x7A3C1E5Bu) sink[blockIdx.x & 1023] = v;
+}
+}  // namespace
+
+hipError_t launch_stream_read(const void* p, int64_t bytes, void* sink, hipStream_t stream) {
+    const int64_t blocks = (bytes + 16383) / 16384;
+    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const char*)p,
+                       (uint32_t)bytes, (uint32_t*)sink);
+    return hipGetLastError();
 }
 
 }  // namespace miqmm

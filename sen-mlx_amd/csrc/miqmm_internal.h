@@ -115,6 +115,7 @@ hipError_t launch_embedding(void* out, const int32_t* ids, int64_t T, const uint
                             int out_dtype, hipStream_t stream);
 hipError_t launch_unpack(uint8_t* codes, const uint32_t* w, int64_t N, int64_t K, int bits,
                          hipStream_t stream);
+hipError_t launch_stream_read(const void* p, int64_t bytes, void* sink, hipStream_t stream);
 hipError_t launch_synth(void* x, uint32_t* w, void* scales, void* biases, int64_t M, int64_t N,
                         int64_t K, int group_size, int bits, int x_dtype, int sb_dtype,
                         uint64_t seed, uint64_t stream_id, hipStream_t stream);

@@ -91,12 +91,13 @@ def lib() -> ctypes.CDLL:
     L.miqmm_quantized_matmul_workspace_size.argtypes = [I64, I64, I64, I, I, ctypes.POINTER(I64)]
     L.miqmm_quantized_matmul_ws.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I, I, I, P, I64, P]
     L.miqmm_quantized_matmul_noalloc.argtypes = [P, P, P, P, P, P, I64, I64, I64, I, I, I, I, I, I, P]
+    L.miqmm_stream_read.argtypes = [P, I64, P, P]
     L.miqmm_gather_qmm_ws.argtypes = [P, P, P, P, P, P, I64, I64, I, I64, I64, I64, I64, I, I, I, I, I, I, I, P,
                                       I64, P]
     for name in ("miqmm_quantized_matmul", "miqmm_quantized_matmul_ex", "miqmm_quantized_linear",
                  "miqmm_dequantize", "miqmm_unpack", "miqmm_query_route", "miqmm_synth_problem",
                  "miqmm_quantized_matmul_grouped", "miqmm_quantized_matmul_workspace_size",
-                 "miqmm_quantized_matmul_ws", "miqmm_quantized_matmul_noalloc"):
+                 "miqmm_quantized_matmul_ws", "miqmm_quantized_matmul_noalloc", "miqmm_stream_read"):
         getattr(L, name).restype = I
     L.miqmm_last_error.argtypes, L.miqmm_last_error.restype = [], ctypes.c_char_p
     L.miqmm_version.argtypes, L.miqmm_version.restype = [], ctypes.c_char_p
@@ -193,6 +194,11 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
                                            K, int(bool(transpose)), group_size, bits, _dt(xc), _dt(scales),
                                            _dt(out), route, _stream(stream)))
     return out
+
+
+def stream_read(buf: torch.Tensor, sink: torch.Tensor, stream=None) -> None:
+    """a plain streaming read of buf (bandwidth ceiling probe; nothing written)"""
+    _check(lib().miqmm_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink), _stream(stream)))
 
 
 def workspace_size(M: int, N: int, K: int, group_size: int = 64, bits: int = 4) -> int:
