@@ -22,6 +22,9 @@ SOURCES = ["qmv.hip", "checkpoint.cpp", "qmv_mfma.hip", "qmvx.hip", "qmm.hip", "
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+    # leading scalar kernel arguments arrive in SGPRs at wave launch (no scalar
+    # memory round trip before a kernel's first load)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

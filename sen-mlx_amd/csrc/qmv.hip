@@ -52,10 +52,20 @@ struct Stage {
     uint32_t xoff;  // byte offset of this chunk in row 0 of x, or kOOB past the row end
 };
 
-// problem p of the kernel-argument table, p wave-uniform: a select chain
-// rather than an index, which would copy the table to scratch
-__device__ __forceinline__ const GemvProblem& pick4(const GemvProblems& P, int p) {
-    return p == 0 ? P.p[0] : p == 1 ? P.p[1] : p == 2 ? P.p[2] : P.p[3];
+// A grouped launch reads its problem table (P.p, in the kernel arguments)
+// with one vector load at entry, dword i of the table into lane i, and takes
+// a field of the tile's problem with v_readlane.  Left to itself
+// the compiler reads the table's tile0 fields, waits, forms a pointer to the
+// chosen entry and reads that: three dependent scalar round trips before the
+// first code load (measured on MI355X: gate/up 896 -> 2 x 4864 at M = 1,
+// 4.50 us grouped against 3.96 us for the same rows as one matrix).
+constexpr int kProblemDwords = (int)(sizeof(GemvProblem) / 4);
+static_assert(sizeof(GemvProblem) % 8 == 0 && kMaxGroup * kProblemDwords <= 64, "one table dword per lane");
+__device__ __forceinline__ uint32_t table_dword(uint32_t tabv, int d) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)tabv, d);
+}
+__device__ __forceinline__ uint64_t table_qword(uint32_t tabv, int d) {
+    return (uint64_t)table_dword(tabv, d) | (uint64_t)table_dword(tabv, d + 1) << 32;
 }
 
 // block barrier over LDS written with ds_write: lgkmcnt(0), then s_barrier,
@@ -101,8 +111,20 @@ constexpr int64_t kMinXTableK = 2048;
 // sum of x), and the stages read their chunk from it; otherwise every stage
 // loads its x chunk and prepares it again.  The same arithmetic on the same
 // values either way: the results are identical bit for bit.
+//
+// Arguments: what the first loads of problem 0 need, as scalars, first (the
+// build preloads the leading kernel arguments into SGPRs at wave launch, so a
+// single-problem wave issues its first loads without a scalar memory round
+// trip; measured on MI355X, a chain of 1 MiB streaming kernels in a HIP
+// graph: 2.41 -> 2.06 us per launch), then y and bias, then the table of
+// every problem (grouped, gather).  meta packs M (bits 0-7), log2 group size
+// (8-15), y dtype (16-23) and ksplit (bit 24); nblocks is the grid size
+// (gridDim would be a load of the implicit arguments).
 template <int BITS, int SBT, int MT, int L, int R, int MODE, bool XL = false>
-__global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, int K, int gs_shift, int y_dtype) {
+__global__ __launch_bounds__(256) void qmv_kernel(const void* x0, const uint32_t* w0, const void* s0, const void* b0,
+                                                  int n0, int tiles, int K, uint32_t meta, int nblocks, void* y0,
+                                                  const void* bias0, const GemvProblems P) {
+    const int M = (int)(meta & 0xff), gs_shift = (int)((meta >> 8) & 0xff), y_dtype = (int)((meta >> 16) & 0xff);
     constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk: 32 or 16
     constexpr int CPC = 1 << CPC_SHIFT;
     constexpr int NP = CPC / 2;
@@ -117,16 +139,25 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     const int sg = lane / L, li = lane % L;
     // wave index, made provably wave-uniform so tile bases live in SGPRs
     const int gwave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-    const int nwaves = gridDim.x * 4;
+    const int nwaves = nblocks * 4;
     const int C = K >> CPC_SHIFT;
     const int J = (C + L - 1) / L;  // chunk iterations per row
-    const int tiles = P.tiles;
+    uint32_t tabv = 0;
+    if constexpr (MODE == 1) {
+        const uint32_t* const tab = reinterpret_cast<const uint32_t*>(&P.p[0]);
+        tabv = tab[lane < kMaxGroup * kProblemDwords ? lane : 0];
+    }
+    constexpr int kW = offsetof(GemvProblem, w) / 4, kS = offsetof(GemvProblem, s) / 4;
+    constexpr int kB = offsetof(GemvProblem, b) / 4, kX = offsetof(GemvProblem, x) / 4;
+    constexpr int kY = offsetof(GemvProblem, y) / 4, kBias = offsetof(GemvProblem, bias) / 4;
+    constexpr int kN = offsetof(GemvProblem, n) / 4, kT0 = offsetof(GemvProblem, tile0) / 4;
     // problem owning a tile (tiles of problem p: [tile0[p], tile0[p+1]))
     auto prob_of = [&](int tile) {
         int p = 0;
         if constexpr (MODE == 1) {
 #pragma unroll
-            for (int i = 1; i < kMaxGroup; ++i) p += (i < P.count && tile >= P.p[i].tile0) ? 1 : 0;
+            for (int i = 1; i < kMaxGroup; ++i)  // an unused slot's tile0 is the tile count: never passed
+                p += tile >= (int)table_dword(tabv, i * kProblemDwords + kT0) ? 1 : 0;
             p = __builtin_amdgcn_readfirstlane(p);
         }
         return p;
@@ -134,9 +165,9 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     // tiles and chunk iterations of this wave: its own tiles over all J chunk
     // passes, or with ksplit the block's tiles over this wave's quarter of them
     const int wv = threadIdx.x >> 6;
-    const bool ks = P.ksplit != 0;
+    const bool ks = (meta >> 24) & 1;
     const int tile_first = ks ? (int)blockIdx.x : gwave;
-    const int tile_stride = ks ? (int)gridDim.x : nwaves;
+    const int tile_stride = ks ? nblocks : nwaves;
     const int j_begin = ks ? wv * J / 4 : 0;
     const int j_count = ks ? (wv + 1) * J / 4 - j_begin : J;
     const int my_tiles = tile_first < tiles ? (tiles - 1 - tile_first) / tile_stride + 1 : 0;
@@ -153,7 +184,6 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     auto locate = [&](int tile) {
         TileRef t;
         if constexpr (MODE == 2) {
-            const GemvProblem& q = P.p[0];
             const int b = __builtin_amdgcn_readfirstlane(tile / P.tiles_per_problem);
             const int lt = tile - b * P.tiles_per_problem;
             // a scalar load: waiting for it leaves the vector loads in flight
@@ -161,26 +191,37 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
             const bool ok = e >= 0 && e < P.experts;  // an index out of range gives zero rows
             const int eb = ok ? e : 0;
             const int xm = P.x_per_expert ? b : b / P.top_k;  // x matrix of this problem
-            t.x = (const uint16_t*)q.x + xm * P.x_stride;
+            t.x = (const uint16_t*)x0 + xm * P.x_stride;
             t.row0 = lt * TILE;
-            t.w = (const char*)q.w + ((size_t)eb * q.n + t.row0) * row_bytes;
-            t.s = (const uint16_t*)q.s + ((size_t)eb * q.n + t.row0) * G;
-            t.b = (const uint16_t*)q.b + ((size_t)eb * q.n + t.row0) * G;
-            t.y = (char*)q.y + b * P.y_stride * ysz;
+            t.w = (const char*)w0 + ((size_t)eb * n0 + t.row0) * row_bytes;
+            t.s = (const uint16_t*)s0 + ((size_t)eb * n0 + t.row0) * G;
+            t.b = (const uint16_t*)b0 + ((size_t)eb * n0 + t.row0) * G;
+            t.y = (char*)y0 + b * P.y_stride * ysz;
             t.bias = nullptr;
-            t.N = q.n;
-            t.rows = ok ? min(q.n - t.row0, TILE) : 0;
+            t.N = n0;
+            t.rows = ok ? min(n0 - t.row0, TILE) : 0;
+        } else if constexpr (MODE == 1) {
+            const int p0 = prob_of(tile) * kProblemDwords;
+            const int n = (int)table_dword(tabv, p0 + kN);
+            t.x = (const void*)table_qword(tabv, p0 + kX);
+            t.row0 = (tile - (int)table_dword(tabv, p0 + kT0)) * TILE;
+            t.w = (const char*)table_qword(tabv, p0 + kW) + (size_t)t.row0 * row_bytes;
+            t.s = (const uint16_t*)table_qword(tabv, p0 + kS) + (size_t)t.row0 * G;
+            t.b = (const uint16_t*)table_qword(tabv, p0 + kB) + (size_t)t.row0 * G;
+            t.y = (char*)table_qword(tabv, p0 + kY);
+            t.bias = (const void*)table_qword(tabv, p0 + kBias);
+            t.N = n;
+            t.rows = min(n - t.row0, TILE);
         } else {
-            const GemvProblem& q = pick4(P, prob_of(tile));
-            t.x = q.x;
-            t.row0 = (tile - q.tile0) * TILE;
-            t.w = (const char*)q.w + (size_t)t.row0 * row_bytes;
-            t.s = (const uint16_t*)q.s + (size_t)t.row0 * G;
-            t.b = (const uint16_t*)q.b + (size_t)t.row0 * G;
-            t.y = (char*)q.y;
-            t.bias = q.bias;
-            t.N = q.n;
-            t.rows = min(q.n - t.row0, TILE);
+            t.x = x0;
+            t.row0 = tile * TILE;
+            t.w = (const char*)w0 + (size_t)t.row0 * row_bytes;
+            t.s = (const uint16_t*)s0 + (size_t)t.row0 * G;
+            t.b = (const uint16_t*)b0 + (size_t)t.row0 * G;
+            t.y = (char*)y0;
+            t.bias = bias0;
+            t.N = n0;
+            t.rows = min(n0 - t.row0, TILE);
         }
         return t;
     };
@@ -354,8 +395,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(const GemvProblems P, int M, i
     }
     if constexpr (XL) {  // build the x table
         float* const xsum = reinterpret_cast<float*>(xtab + (C + 1) * NQ);
-        const auto xr = make_rsrc(P.p[0].x, (uint32_t)K * 2);
-        for (int c = threadIdx.x; c <= C; c += blockDim.x) {
+        const auto xr = make_rsrc(x0, (uint32_t)K * 2);
+        for (int c = threadIdx.x; c <= C; c += 256) {
             uint32_t xw[NP], X[NP];
 #pragma unroll
             for (int i = 0; i < NQ; ++i) {
@@ -411,6 +452,12 @@ int gemv_blocks(int64_t tiles, int ksplit, int per_cu = kMaxBlocksPerCU) {
     return (int)(want < (int64_t)num_cus() * per_cu ? want : (int64_t)num_cus() * per_cu);
 }
 
+// the kernel's meta argument: M, log2 group size, y dtype, ksplit
+uint32_t pack_meta(const QmmArgs& a, int ksplit) {
+    return (uint32_t)a.M | (uint32_t)__builtin_ctz((unsigned)a.group_size) << 8 | (uint32_t)a.y_dtype << 16 |
+           (uint32_t)(ksplit ? 1 : 0) << 24;
+}
+
 // a[0..count) share M, K, group size, bits and dtypes; one grid covers all
 // (grouped grids are built for one or two rows of x only)
 template <int BITS, int SBT, int MT, int L, int R>
@@ -421,14 +468,15 @@ hipError_t launch_t(const QmmArgs* a, int count) {
     P.count = count;
     int64_t tiles = 0;
     for (int i = 0; i < kMaxGroup; ++i) {
-        const QmmArgs& q = a[i < count ? i : count - 1];  // unused slots repeat the last problem
+        const QmmArgs& q = a[i < count ? i : count - 1];  // unused slots: the last problem, tile0 = the tile count
         P.p[i] = GemvProblem{q.x, q.w, q.scales, q.biases, q.y, q.bias, (int)q.N, (int)tiles};
         if (i < count) tiles += (q.N + TILE - 1) / TILE;
     }
     P.tiles = (int)tiles;
     P.ksplit = use_ksplit(tiles, a[0].K, a[0].bits, L);
     const int blocks = gemv_blocks(tiles, P.ksplit);
-    const int gs_shift = __builtin_ctz((unsigned)a[0].group_size);
+    const uint32_t meta = pack_meta(a[0], P.ksplit);
+    const GemvProblem& p0 = P.p[0];
     if constexpr (MT == 1) {  // one row of x shared by every problem: the LDS x table
         bool shared = true;
         for (int i = 1; i < count; ++i) shared = shared && a[i].x == a[0].x;
@@ -436,22 +484,22 @@ hipError_t launch_t(const QmmArgs* a, int count) {
         if (shared && !P.ksplit && a[0].K >= kMinXTableK && xt <= kMaxXTable) {
             if (count > 1)
                 hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 1, true>), dim3(blocks), dim3(256), (size_t)xt,
-                                   a[0].stream, P, (int)a[0].M, (int)a[0].K, gs_shift, a[0].y_dtype);
+                                   a[0].stream, p0.x, p0.w, p0.s, p0.b, p0.n, P.tiles, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
             else
                 hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 0, true>), dim3(blocks), dim3(256), (size_t)xt,
-                                   a[0].stream, P, (int)a[0].M, (int)a[0].K, gs_shift, a[0].y_dtype);
+                                   a[0].stream, p0.x, p0.w, p0.s, p0.b, p0.n, P.tiles, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
             return hipGetLastError();
         }
     }
     if constexpr (MT <= 2) {
         if (count > 1) {
-            hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 1>), dim3(blocks), dim3(256), 0, a[0].stream, P,
-                               (int)a[0].M, (int)a[0].K, gs_shift, a[0].y_dtype);
+            hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 1>), dim3(blocks), dim3(256), 0, a[0].stream, p0.x,
+                               p0.w, p0.s, p0.b, p0.n, P.tiles, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 0>), dim3(blocks), dim3(256), 0, a[0].stream, P,
-                       (int)a[0].M, (int)a[0].K, gs_shift, a[0].y_dtype);
+    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 0>), dim3(blocks), dim3(256), 0, a[0].stream, p0.x, p0.w,
+                       p0.s, p0.b, p0.n, P.tiles, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
     return hipGetLastError();
 }
 
@@ -475,9 +523,9 @@ hipError_t launch_gather_t(const QmmArgs& a, const int32_t* idx, int64_t T, int 
     P.tiles = (int)tiles;
     P.ksplit = use_ksplit(tiles, a.K, a.bits, L);
     const int blocks = gemv_blocks(tiles, P.ksplit, kMaxGatherBlocksPerCU);
-    const int gs_shift = __builtin_ctz((unsigned)a.group_size);
-    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 2>), dim3(blocks), dim3(256), 0, a.stream, P, (int)a.M,
-                       (int)a.K, gs_shift, a.y_dtype);
+    const GemvProblem& p0 = P.p[0];
+    hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 2>), dim3(blocks), dim3(256), 0, a.stream, p0.x, p0.w, p0.s,
+                       p0.b, p0.n, P.tiles, (int)a.K, pack_meta(a, P.ksplit), blocks, p0.y, p0.bias, P);
     return hipGetLastError();
 }
 

@@ -167,8 +167,16 @@ __device__ __forceinline__ float transposed_sum(float (&v)[RB], int lane) {
 template <int RB>
 constexpr int max_threads() { return RB >= 32 ? 512 : 1024; }  // 32 rows of codes take 128 registers
 
+// The arguments are scalars, the ones the first loads need leading: the build
+// preloads leading kernel arguments into SGPRs at wave launch, which spares
+// the scalar memory round trip before the first load (bias, read last, is
+// past the preloaded registers).  meta = log2 group size | y dtype << 8 |
+// waves per block << 16 (blockDim would be a load of the implicit arguments).
 template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS>
-__global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const QmvsArgs P) {
+__global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t* xp, const uint32_t* wp,
+                                                                 const uint16_t* sp, const uint16_t* bp, int n, int k,
+                                                                 uint32_t meta, void* yp, const void* biasp) {
+    const QmvsArgs P{xp, wp, sp, bp, yp, biasp, n, k, (int)(meta & 0xff), (int)((meta >> 8) & 0xff)};
     constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk: 32 or 16
     constexpr int CPC = 1 << CPC_SHIFT;
     constexpr int NP = CPC / 2;                   // bf16 pairs of x per chunk
@@ -177,7 +185,7 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const QmvsArgs 
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int lane = threadIdx.x & 63;
     const int ws = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's K-slice
-    const int KS = blockDim.x >> 6;
+    const int KS = (int)(meta >> 16);
     const int K = P.K, gs_shift = P.gs_shift;
     const int C = K >> CPC_SHIFT;       // chunks per row
     const int c = ws * 64 + lane;       // this lane's chunk of every row
@@ -410,7 +418,8 @@ hipError_t launch_t(const QmmArgs& a, int ks) {
                      (int)a.N, (int)a.K, __builtin_ctz((unsigned)a.group_size), a.y_dtype};
     const size_t lds = (size_t)ks * wave_lds<ND>() + (size_t)ks * RB * 4;
     const int blocks = (int)((a.N + RB - 1) / RB);
-    hipLaunchKernelGGL((qmvs_kernel<BITS, SBT, RB, ND, YF32, BIAS>), dim3(blocks), dim3(64 * ks), lds, a.stream, P);
+    hipLaunchKernelGGL((qmvs_kernel<BITS, SBT, RB, ND, YF32, BIAS>), dim3(blocks), dim3(64 * ks), lds, a.stream, P.x,
+                       P.w, P.s, P.b, P.N, P.K, (uint32_t)P.gs_shift | (uint32_t)P.y_dtype << 8 | (uint32_t)ks << 16, P.y, P.bias);
     return hipGetLastError();
 }
 
