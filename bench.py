@@ -10,8 +10,10 @@ gate 896->4864, up 896->4864, down 4864->896} + lm_head 896->151936.  Weights
 are random (seeded, generated on the device); x ~ N(0,1) is drawn per layer
 input, as in the model: q, k and v read the attention input, gate and up the
 MLP input, o and down their own.  q/k/v and gate/up run as one grouped call
-each: 97 launches per step, captured once per weight replica into a HIP
-graph; three replicas (838 MB) rotate so no step finds its weights in the
+each, their weights stored contiguously per layer (as a loader that fuses
+them lays them out; the same step on separately allocated weights, and with
+one launch per projection, is reported beside it): 97 launches per step,
+captured once per weight replica into a HIP graph; three replicas (838 MB) rotate so no step finds its weights in the
 256 MB Infinity Cache.  W untimed steps, then exactly K timed steps between
 two device synchronizations, with HIP events on the replay stream.
 
@@ -83,17 +85,38 @@ class Proj:
     __slots__ = ("name", "N", "K", "x", "w", "s", "b", "y")
 
 
-def make_replica(miqmm, torch, replica, shapes):
+def split_rows(miqmm, torch, Ns, K, seed, stream_id):
+    """projections stored one after another, as a loader that fuses q/k/v or
+    gate/up lays them out: one generated matrix of sum(Ns) rows, returned as
+    row views (x, [(w, s, b) per projection])"""
+    x, w, s, b = miqmm.synth_problem(1, sum(Ns), K, 64, 4, seed=seed, stream_id=stream_id)
+    views, o = [], 0
+    for N in Ns:
+        views.append((w[o:o + N], s[o:o + N], b[o:o + N]))
+        o += N
+    return x, views
+
+
+def make_replica(miqmm, torch, replica, shapes, fused=True):
+    """one set of the step's weights; fused: each layer's q/k/v and gate/up
+    stored contiguously (row views of one matrix), else every projection in
+    its own allocation"""
     projs = []
     for i, (name, N, K) in enumerate(shapes):
         p = Proj()
         p.name, p.N, p.K = name, N, K
-        p.x, p.w, p.s, p.b = miqmm.synth_problem(1, N, K, 64, 4, seed=replica, stream_id=i)
+        if not fused or not (name.endswith((".q", ".k", ".v", ".gate", ".up"))):
+            p.x, p.w, p.s, p.b = miqmm.synth_problem(1, N, K, 64, 4, seed=replica, stream_id=i)
         p.y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
         projs.append(p)
-    # one x per layer input: k and v read q's input, up reads gate's
     for layer in range(QWEN05_LAYERS):
         q, k, v, o, gate, up, down = projs[layer * 7:layer * 7 + 7]
+        if fused:
+            for grp, sid in (((q, k, v), layer * 7), ((gate, up), layer * 7 + 4)):
+                x, views = split_rows(miqmm, torch, [p.N for p in grp], grp[0].K, replica, sid)
+                for p, (w, s_, b) in zip(grp, views):
+                    p.x, p.w, p.s, p.b = x, w, s_, b
+        # one x per layer input: k and v read q's input, up reads gate's
         k.x = v.x = q.x
         up.x = gate.x
     return projs
@@ -215,20 +238,26 @@ def line(sec, nb):
     return {"us": round(sec * 1e6, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": nb}
 
 
-def step_type_line(miqmm, torch, Ns, K, reps=REPS):
-    """one of the step's launch types on its own: grouped projections (shared x)
-    or a single one, cold replicas; (seconds per launch, algorithmic bytes per launch)"""
+def step_type_line(miqmm, torch, Ns, K, reps=REPS, fused=True):
+    """one of the step's launch types on its own: grouped projections (shared x;
+    fused: stored contiguously, as in the step) or a single one, cold
+    replicas; (seconds per launch, algorithmic bytes per launch)"""
     nb = group_bytes(Ns, K) if len(Ns) > 1 else qbytes(1, Ns[0], K)
     groups = []
     for r in range(replicas_for(nb)):
-        x = None
         grp = []
-        for j, N in enumerate(Ns):
+        if fused and len(Ns) > 1:
+            x, views = split_rows(miqmm, torch, Ns, K, 200 + r, sum(Ns))
+        else:
+            x, views = None, [None] * len(Ns)
+        for j, (N, v) in enumerate(zip(Ns, views)):
             p = Proj()
             p.N, p.K = N, K
-            p.x, p.w, p.s, p.b = miqmm.synth_problem(1, N, K, 64, 4, seed=200 + r, stream_id=10 * j + N)
-            if x is None:
-                x = p.x
+            if v is None:
+                p.x, p.w, p.s, p.b = miqmm.synth_problem(1, N, K, 64, 4, seed=200 + r, stream_id=10 * j + N)
+                x = p.x if x is None else x
+            else:
+                p.w, p.s, p.b = v
             p.x = x
             p.y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
             grp.append(p)
@@ -418,7 +447,7 @@ def step_types(miqmm, torch):
         r = line(sec, nb)
         r["launches_per_step"] = count
         r["us_per_step"] = round(sec * 1e6 * count, 2)
-        r["route"] = miqmm.query_route(1, Ns[0], K, 64, 4)[0] if len(Ns) == 1 else "grouped v_dot2"
+        r["route"] = miqmm.query_route(1, Ns[0], K, 64, 4)[0] if len(Ns) == 1 else "grouped v_dot2, contiguous"
         res[name] = r
         torch.cuda.empty_cache()
     return res
@@ -516,6 +545,18 @@ def main():
               "GB/s": round(step_bytes_single * args.steps / t1 / 1e9, 2), "bytes_per_step": step_bytes_single}
     del graphs, replicas
     torch.cuda.empty_cache()
+    # the same grouped step with every projection in its own allocation
+    replicas = [make_replica(miqmm, torch, r, shapes, fused=False) for r in range(args.replicas)]
+    for projs in replicas:
+        run_step_grouped(miqmm, projs)
+    torch.cuda.synchronize()
+    graphs = [capture(torch, (lambda p=projs: run_step_grouped(miqmm, p))) for projs in replicas]
+    time_graphs(torch, graphs, max(args.warmup, 1))
+    t2 = time_graphs(torch, graphs, args.steps)
+    separate = {"us_per_step": round(t2 / args.steps * 1e6, 2), "launches": 97,
+                "GB/s": round(step_bytes * args.steps / t2 / 1e9, 2), "bytes_per_step": step_bytes}
+    del graphs, replicas
+    torch.cuda.empty_cache()
 
     # the step's launch types on their own; the roofline kernel is the one with the most time per step
     types = step_types(miqmm, torch)
@@ -529,7 +570,8 @@ def main():
         "config": {"workload": "qwen2.5-0.5b decode step, linear layers only: 24 x {q 896->896, k 896->128, "
                                "v 896->128, o 896->896, gate 896->4864, up 896->4864, down 4864->896} + "
                                "lm_head 896->151936; M=1, 4-bit, group 64, bf16 x/scales/biases/y; "
-                               "q/k/v and gate/up as one grouped call each",
+                               "q/k/v and gate/up as one grouped call each, each layer's q/k/v and gate/up "
+                               "weights stored contiguously (fused at load)",
                    "launches_per_step": 97, "bytes_per_step": step_bytes,
                    "weight_replicas": args.replicas, "hip_graph": True},
         "roofline": {"kernel": f"{dom}: the step's launch type with the most time per step "
@@ -540,9 +582,11 @@ def main():
                      "avg_launch_us": d["us"], "bytes_per_launch": d["bytes"]},
         "step_types": types,
         "step_one_launch_per_projection": single,
+        "step_grouped_separate_allocations": separate,
     }
     print(f"# step {ms_per_step * 1e3:.1f} us, {gbs:.1f} GB/s (one launch per projection: "
-          f"{single['us_per_step']:.1f} us); types {json.dumps(types)}", file=sys.stderr, flush=True)
+          f"{single['us_per_step']:.1f} us; grouped, separate allocations: {separate['us_per_step']:.1f} us); "
+          f"types {json.dumps(types)}", file=sys.stderr, flush=True)
     torch.cuda.empty_cache()
 
     if not args.no_headline:

@@ -118,8 +118,12 @@ constexpr int64_t kMinXTableK = 2048;
 // trip; measured on MI355X, a chain of 1 MiB streaming kernels in a HIP
 // graph: 2.41 -> 2.06 us per launch), then y and bias, then the table of
 // every problem (grouped, gather).  meta packs M (bits 0-7), log2 group size
-// (8-15), y dtype (16-23) and ksplit (bit 24); nblocks is the grid size
-// (gridDim would be a load of the implicit arguments).
+// (8-15), y dtype (16-23), ksplit (bit 24) and contiguous (bit 25); nblocks
+// is the grid size (gridDim would be a load of the implicit arguments).
+// Contiguous (grouped only): the problems' codes, scales and biases follow
+// one another in memory, every problem but the last fills whole row tiles and
+// all read the same x, so the loads treat them as one matrix of n0 rows from
+// the scalar bases, and only the stores look up their problem in the table.
 template <int BITS, int SBT, int MT, int L, int R, int MODE, bool XL = false>
 __global__ __launch_bounds__(256) void qmv_kernel(const void* x0, const uint32_t* w0, const void* s0, const void* b0,
                                                   int n0, int tiles, int K, uint32_t meta, int nblocks, void* y0,
@@ -181,9 +185,22 @@ __global__ __launch_bounds__(256) void qmv_kernel(const void* x0, const uint32_t
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
     const int ysz = y_dtype == DT_F32 ? 4 : 2;
-    auto locate = [&](int tile) {
+    const bool contig = MODE == 1 && ((meta >> 25) & 1);
+    // the tile's bases; `store`: where its results go (contiguous groups read
+    // from the scalar bases and store through the table)
+    auto locate = [&](int tile, bool store) {
         TileRef t;
-        if constexpr (MODE == 2) {
+        if (MODE == 0 || (contig && !store)) {
+            t.x = x0;
+            t.row0 = tile * TILE;
+            t.w = (const char*)w0 + (size_t)t.row0 * row_bytes;
+            t.s = (const uint16_t*)s0 + (size_t)t.row0 * G;
+            t.b = (const uint16_t*)b0 + (size_t)t.row0 * G;
+            t.y = (char*)y0;
+            t.bias = bias0;
+            t.N = n0;
+            t.rows = min(n0 - t.row0, TILE);
+        } else if constexpr (MODE == 2) {
             const int b = __builtin_amdgcn_readfirstlane(tile / P.tiles_per_problem);
             const int lt = tile - b * P.tiles_per_problem;
             // a scalar load: waiting for it leaves the vector loads in flight
@@ -212,16 +229,6 @@ __global__ __launch_bounds__(256) void qmv_kernel(const void* x0, const uint32_t
             t.bias = (const void*)table_qword(tabv, p0 + kBias);
             t.N = n;
             t.rows = min(n - t.row0, TILE);
-        } else {
-            t.x = x0;
-            t.row0 = tile * TILE;
-            t.w = (const char*)w0 + (size_t)t.row0 * row_bytes;
-            t.s = (const uint16_t*)s0 + (size_t)t.row0 * G;
-            t.b = (const uint16_t*)b0 + (size_t)t.row0 * G;
-            t.y = (char*)y0;
-            t.bias = bias0;
-            t.N = n0;
-            t.rows = min(n0 - t.row0, TILE);
         }
         return t;
     };
@@ -269,7 +276,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const void* x0, const uint32_t
             j_i = 0;
             tile_i += tile_stride;
         }
-        const TileRef t = locate(tile);
+        const TileRef t = locate(tile, false);
         const uint32_t valid_rows = (uint32_t)t.rows;
         // resources rebased on the tile: 32-bit offsets, and rows past N read as zero
         const auto wr = make_rsrc(t.w, valid_rows * row_bytes);
@@ -313,7 +320,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const void* x0, const uint32_t
             prep_x(st.xw, X, xs);
         } else {
             uint32_t xw[MT][NP];
-            load_x(make_rsrc(locate(tile_c).x, (uint32_t)M * xrow_bytes), st.xoff, xw);
+            load_x(make_rsrc(locate(tile_c, false).x, (uint32_t)M * xrow_bytes), st.xoff, xw);
             prep_x(xw, X, xs);
         }
 #pragma unroll
@@ -337,7 +344,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(const void* x0, const uint32_t
             }
         }
         if (++j_c == j_count) {  // tile complete: reduce over the sub-group and store
-            const TileRef tc = locate(tile_c);
+            const TileRef tc = locate(tile_c, true);
             const int N = tc.N;
             void* const y = tc.y;
             const void* const bias = tc.bias;
@@ -458,6 +465,29 @@ uint32_t pack_meta(const QmmArgs& a, int ksplit) {
            (uint32_t)(ksplit ? 1 : 0) << 24;
 }
 
+int64_t total_rows(const QmmArgs* a, int count) {
+    int64_t n = 0;
+    for (int i = 0; i < count; ++i) n += a[i].N;
+    return n;
+}
+
+// whether the problems' codes, scales and biases each continue the previous
+// problem's, every problem but the last fills whole tiles of `tile` rows and
+// all share x: the kernel then loads them as one matrix
+bool contiguous_group(const QmmArgs* a, int count, int tile) {
+    const int64_t row_bytes = a[0].K * a[0].bits / 8, sb_row = a[0].K / a[0].group_size * 2;
+    int64_t rows = 0;
+    for (int i = 0; i < count; ++i) {
+        if (a[i].x != a[0].x) return false;
+        if ((const char*)a[i].w != (const char*)a[0].w + rows * row_bytes) return false;
+        if ((const char*)a[i].scales != (const char*)a[0].scales + rows * sb_row) return false;
+        if ((const char*)a[i].biases != (const char*)a[0].biases + rows * sb_row) return false;
+        if (i + 1 < count && a[i].N % tile != 0) return false;
+        rows += a[i].N;
+    }
+    return rows < ((int64_t)1 << 31);
+}
+
 // a[0..count) share M, K, group size, bits and dtypes; one grid covers all
 // (grouped grids are built for one or two rows of x only)
 template <int BITS, int SBT, int MT, int L, int R>
@@ -472,11 +502,14 @@ hipError_t launch_t(const QmmArgs* a, int count) {
         P.p[i] = GemvProblem{q.x, q.w, q.scales, q.biases, q.y, q.bias, (int)q.N, (int)tiles};
         if (i < count) tiles += (q.N + TILE - 1) / TILE;
     }
+    if (tiles >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
     P.tiles = (int)tiles;
     P.ksplit = use_ksplit(tiles, a[0].K, a[0].bits, L);
     const int blocks = gemv_blocks(tiles, P.ksplit);
-    const uint32_t meta = pack_meta(a[0], P.ksplit);
-    const GemvProblem& p0 = P.p[0];
+    GemvProblem p0 = P.p[0];
+    const bool contig = count > 1 && contiguous_group(a, count, TILE);
+    if (contig) p0.n = (int)total_rows(a, count);  // the loads' one matrix
+    const uint32_t meta = pack_meta(a[0], P.ksplit) | (contig ? 1u << 25 : 0u);
     if constexpr (MT == 1) {  // one row of x shared by every problem: the LDS x table
         bool shared = true;
         for (int i = 1; i < count; ++i) shared = shared && a[i].x == a[0].x;
