@@ -119,14 +119,17 @@ constexpr int64_t kMinXTableK = 2048;
 // graph: 2.41 -> 2.06 us per launch), then y and bias, then the table of
 // every problem (grouped, gather).  meta packs M (bits 0-7), log2 group size
 // (8-15), y dtype (16-23), ksplit (bit 24) and contiguous (bit 25); nblocks
-// is the grid size (gridDim would be a load of the implicit arguments).
+// is the grid size (gridDim would be a load of the implicit arguments); tq
+// and tr are the quotient and remainder of the tile count by the tile stride
+// (nblocks with ksplit, else 4 nblocks), so a wave counts its tiles without
+// a division.
 // Contiguous (grouped only): the problems' codes, scales and biases follow
 // one another in memory, every problem but the last fills whole row tiles and
 // all read the same x, so the loads treat them as one matrix of n0 rows from
 // the scalar bases, and only the stores look up their problem in the table.
 template <int BITS, int SBT, int MT, int L, int R, int MODE, bool XL = false>
 __global__ __launch_bounds__(256) void qmv_kernel(const void* x0, const uint32_t* w0, const void* s0, const void* b0,
-                                                  int n0, int tiles, int K, uint32_t meta, int nblocks, void* y0,
+                                                  int n0, int tq, int tr, int K, uint32_t meta, int nblocks, void* y0,
                                                   const void* bias0, const GemvProblems P) {
     const int M = (int)(meta & 0xff), gs_shift = (int)((meta >> 8) & 0xff), y_dtype = (int)((meta >> 16) & 0xff);
     constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk: 32 or 16
@@ -168,13 +171,13 @@ __global__ __launch_bounds__(256) void qmv_kernel(const void* x0, const uint32_t
     };
     // tiles and chunk iterations of this wave: its own tiles over all J chunk
     // passes, or with ksplit the block's tiles over this wave's quarter of them
-    const int wv = threadIdx.x >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool ks = (meta >> 24) & 1;
     const int tile_first = ks ? (int)blockIdx.x : gwave;
     const int tile_stride = ks ? nblocks : nwaves;
     const int j_begin = ks ? wv * J / 4 : 0;
     const int j_count = ks ? (wv + 1) * J / 4 - j_begin : J;
-    const int my_tiles = tile_first < tiles ? (tiles - 1 - tile_first) / tile_stride + 1 : 0;
+    const int my_tiles = tq + (tile_first < tr ? 1 : 0);
     const int iters = my_tiles * j_count;
     // x table: quad q of chunk c at quad c*NQ + (q + (c >> ROT)) % NQ, so the
     // quads that 16 lanes read from 16 consecutive chunks cover all 64 banks;
@@ -503,6 +506,7 @@ hipError_t launch_t(const QmmArgs* a, int count) {
         if (i < count) tiles += (q.N + TILE - 1) / TILE;
     }
     if (tiles >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    if (tiles == 0) return hipSuccess;
     P.tiles = (int)tiles;
     P.ksplit = use_ksplit(tiles, a[0].K, a[0].bits, L);
     const int blocks = gemv_blocks(tiles, P.ksplit);
@@ -510,6 +514,7 @@ hipError_t launch_t(const QmmArgs* a, int count) {
     const bool contig = count > 1 && contiguous_group(a, count, TILE);
     if (contig) p0.n = (int)total_rows(a, count);  // the loads' one matrix
     const uint32_t meta = pack_meta(a[0], P.ksplit) | (contig ? 1u << 25 : 0u);
+    const int stride = P.ksplit ? blocks : 4 * blocks, tq = (int)(tiles / stride), tr = (int)(tiles % stride);
     if constexpr (MT == 1) {  // one row of x shared by every problem: the LDS x table
         bool shared = true;
         for (int i = 1; i < count; ++i) shared = shared && a[i].x == a[0].x;
@@ -517,22 +522,22 @@ hipError_t launch_t(const QmmArgs* a, int count) {
         if (shared && !P.ksplit && a[0].K >= kMinXTableK && xt <= kMaxXTable) {
             if (count > 1)
                 hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 1, true>), dim3(blocks), dim3(256), (size_t)xt,
-                                   a[0].stream, p0.x, p0.w, p0.s, p0.b, p0.n, P.tiles, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
+                                   a[0].stream, p0.x, p0.w, p0.s, p0.b, p0.n, tq, tr, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
             else
                 hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 0, true>), dim3(blocks), dim3(256), (size_t)xt,
-                                   a[0].stream, p0.x, p0.w, p0.s, p0.b, p0.n, P.tiles, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
+                                   a[0].stream, p0.x, p0.w, p0.s, p0.b, p0.n, tq, tr, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
             return hipGetLastError();
         }
     }
     if constexpr (MT <= 2) {
         if (count > 1) {
             hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 1>), dim3(blocks), dim3(256), 0, a[0].stream, p0.x,
-                               p0.w, p0.s, p0.b, p0.n, P.tiles, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
+                               p0.w, p0.s, p0.b, p0.n, tq, tr, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
             return hipGetLastError();
         }
     }
     hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 0>), dim3(blocks), dim3(256), 0, a[0].stream, p0.x, p0.w,
-                       p0.s, p0.b, p0.n, P.tiles, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
+                       p0.s, p0.b, p0.n, tq, tr, (int)a[0].K, meta, blocks, p0.y, p0.bias, P);
     return hipGetLastError();
 }
 
@@ -553,12 +558,15 @@ hipError_t launch_gather_t(const QmmArgs& a, const int32_t* idx, int64_t T, int 
     P.y_stride = y_stride;
     const int64_t tiles = (int64_t)P.tiles_per_problem * T * top_k;
     if (tiles >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    if (tiles == 0) return hipSuccess;
     P.tiles = (int)tiles;
     P.ksplit = use_ksplit(tiles, a.K, a.bits, L);
     const int blocks = gemv_blocks(tiles, P.ksplit, kMaxGatherBlocksPerCU);
+    const int64_t stride = P.ksplit ? blocks : 4 * blocks;
     const GemvProblem& p0 = P.p[0];
     hipLaunchKernelGGL((qmv_kernel<BITS, SBT, MT, L, R, 2>), dim3(blocks), dim3(256), 0, a.stream, p0.x, p0.w, p0.s,
-                       p0.b, p0.n, P.tiles, (int)a.K, pack_meta(a, P.ksplit), blocks, p0.y, p0.bias, P);
+                       p0.b, p0.n, (int)(tiles / stride), (int)(tiles % stride), (int)a.K, pack_meta(a, P.ksplit),
+                       blocks, p0.y, p0.bias, P);
     return hipGetLastError();
 }
 
