@@ -155,6 +155,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 constexpr uint32_t kOOB = 0x80000000u;  // an offset past any resource this library builds
 
+// s_waitcnt immediate: vmcnt(n), expcnt and lgkmcnt left unconstrained
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// LDS destination of a direct-to-LDS buffer load
+typedef __attribute__((address_space(3))) void lds_void;
+
 __device__ __forceinline__ u32x4_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }

@@ -101,8 +101,6 @@ __device__ __forceinline__ uint32_t lds_off(int R, int r, int kk, int fk) {
     return kk * R * 32 + r * 32 + ((fk ^ ((r >> 3) & 1)) << 4);
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 template <int BITS, int W_PER>
 struct WRegs {
     u32x4_t q[W_PER];

@@ -32,6 +32,15 @@
 // waves split K into contiguous k-quad ranges (a k-quad is 4 k-blocks = 128
 // codes) and combine their partial sums through LDS at the end.
 //
+// Scales and biases: each wave copies those of its k range for the block's
+// rows into its own LDS area when it starts (direct-to-LDS dword loads, ahead
+// of the first stages' loads), so a group cycle's dequant reads LDS.  Read
+// from memory at the cycle's end instead, the wait for them drains every
+// stage in flight with them (measured on MI355X, 4-bit g64: M = 16, 4096 ->
+// 14336 31.3 -> 26.7 us, 14336 -> 4096 36.2 -> 26.3 us; M = 8, 14336 ->
+// 4096 28.8 -> 19.5 us).  Odd G or scales not 4-byte aligned keep the
+// memory reads.
+//
 // Loads: 4-bit -- lane (n, q) loads 16 bytes = chunk 4u+q (k-block 4u+q) of
 // row n, so the 4 lanes of a row read 64 contiguous bytes; a 4x4 transpose of
 // words across the lane quarters (v_permlane32_swap, v_permlane16_swap) then
@@ -40,6 +49,7 @@
 // k-block directly.  All loads are raw buffer loads with 32-bit offsets from
 // per-block bases; offsets past the end read as zero, which masks ragged K,
 // ragged N and the A rows of inactive group slots.
+#include <atomic>
 #include <type_traits>
 
 #include "miqmm_device.h"
@@ -64,6 +74,15 @@ __device__ __forceinline__ void transpose4x4(u32x4_t& v) {
     v[2] = d[0];
     v[3] = d[1];
 }
+
+// group pairs per row that a wave stages (its k range, QS k-quads of 128
+// codes, starting at an even group), and the pairs of one array (scales or
+// biases) of a wave's LDS area: rows x pairs, rounded up to whole 64-lane
+// direct-to-LDS loads
+__host__ __device__ constexpr int sb_pairs(int K, int gs_shift, int wpb) {
+    return ((((K >> 5) + 3) >> 2) + wpb - 1) / wpb * (128 >> gs_shift) / 2 + 1;
+}
+__host__ __device__ constexpr int sb_area_pairs(int T, int npr) { return (16 * T * npr + 63) / 64 * 64; }
 
 template <int BITS, int T>
 struct QStage {
@@ -97,14 +116,17 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
                                                             const uint16_t* __restrict__ bi,
                                                             void* __restrict__ y,
                                                             const void* __restrict__ bias, int M, int N,
-                                                            int K, int gs_shift, int y_dtype,
+                                                            int K, int gs_shift, int y_dtype, int sbl,
                                                             const MfmaGather g = MfmaGather{}) {
     constexpr int GS = 16 / MT;                 // group slots per m
     constexpr int NMT = MT >= 4 ? MT / 4 : 1;   // distinct m per lane
     constexpr float kCentre = BITS == 4 ? 128.f : 0.f;
     using St = QStage<BITS, T>;
+    // vector-memory loads of one stage: the codes (4-bit: one per tile;
+    // 8-bit: two 8-byte loads per tile and register) and four x loads
+    constexpr int kStageLoads = (BITS == 4 ? T : 4 * T) + 4;
 
-    extern __shared__ float red[];  // [WPB][T][64 lanes][NMT]
+    extern __shared__ float red[];  // [WPB][T][64 lanes][NMT], then the waves' scale / bias areas
 
     const int lane = threadIdx.x & 63;
     const int nl = lane & 15, q = lane >> 4;
@@ -192,6 +214,12 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
     // GS < 4 only GS of them differ (r % GS = j % GS), so each distinct
     // scale / bias is loaded once (M = 16: one pair per row instead of four)
     constexpr int NG = GS < 4 ? GS : 4;
+    // this wave's LDS area: scales then biases, [16T rows][2 npr] halves of
+    // groups g0 .. g0 + 2 npr - 1 (g0 even), zero past G
+    const int npr = sb_pairs(K, gs_shift, WPB), area = sb_area_pairs(T, npr);
+    const int g0 = (u0 << (7 - gs_shift)) & ~1;
+    uint16_t* const sl = reinterpret_cast<uint16_t*>(red + WPB * T * 64 * NMT) + wv * 4 * area;
+    uint16_t* const bl = sl + 2 * area;
     auto rescale = [&](int c) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
@@ -200,9 +228,20 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
 #pragma unroll
             for (int jj = 0; jj < NG; ++jj) {
                 const int g = c * GS + ((4 * q + jj) % GS);
-                const uint32_t off = g < G ? (row * G + g) * 2 : kOOB;
-                sv[jj] = half_to_f32<SBT>(bload2(sr, off));
-                bv[jj] = half_to_f32<SBT>(bload2(br, off)) - kCentre * sv[jj];
+                uint16_t sh, bh;
+                if (sbl) {  // groups of the cycle outside this wave's range have no codes here: zero
+                    const int gi = g - g0;
+                    const bool in = g < G && gi >= 0 && gi < 2 * npr;
+                    const int li = in ? (int)row * 2 * npr + gi : 0;
+                    sh = in ? sl[li] : 0;
+                    bh = in ? bl[li] : 0;
+                } else {
+                    const uint32_t off = g < G ? (row * G + g) * 2 : kOOB;
+                    sh = bload2(sr, off);
+                    bh = bload2(br, off);
+                }
+                sv[jj] = half_to_f32<SBT>(sh);
+                bv[jj] = half_to_f32<SBT>(bh) - kCentre * sv[jj];
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -259,9 +298,25 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
     // issue makes the compiler's wait before each compute count from the path
     // without the loads, i.e. wait for the stage just issued.
     if (u0 < u1) {
+        if (sbl) {  // stage the scales and biases, ahead of the stages' loads
+            const int npairs = 16 * T * npr;
+            for (int d = 0; d * 64 < npairs; ++d) {
+                const int e = d * 64 + lane;
+                const int row = e / npr, gp = g0 + 2 * (e - row * npr);
+                const uint32_t off = e < npairs && gp < G ? ((uint32_t)row * G + gp) * 2 : kOOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(sl + 128 * d), 4, off, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (lds_void*)(bl + 128 * d), 4, off, 0, 0, 0);
+            }
+        }
         St A, B;
         issue(u0, A);
         issue(u0 + 1, B);
+        // the staged scales land before any cycle reads them (the compiler
+        // does not see that dependency): issued after them and still allowed
+        // in flight are the two stages' loads
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kStageLoads));
+        asm volatile("" ::: "memory");
         int u = u0;
         for (; u + 2 <= u1; u += 2) {
             compute(u, A);
@@ -304,15 +359,44 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
     }
 }
 
+// LDS of a launch: the cross-wave reduction, and the waves' scale / bias
+// areas when they stage them (an even number of groups per row, 4-byte
+// aligned arrays: the copies move group pairs; and room in the 160 KiB)
+size_t mfma_lds(const QmmArgs& a, int T, int wpb, int nmt, int* sbl) {
+    const size_t red = sizeof(float) * wpb * T * 64 * nmt;
+    const int npr = sb_pairs((int)a.K, __builtin_ctz((unsigned)a.group_size), wpb);
+    const size_t stage = (size_t)wpb * 2 * sb_area_pairs(T, npr) * 4;
+    const bool al = ((reinterpret_cast<uintptr_t>(a.scales) | reinterpret_cast<uintptr_t>(a.biases)) & 3) == 0;
+    *sbl = (a.K / a.group_size) % 2 == 0 && al && red + stage <= 160 * 1024 ? 1 : 0;
+    return red + (*sbl ? stage : 0);
+}
+// dynamic LDS above the default 64 KiB needs the kernel's attribute raised,
+// once per kernel and device (two threads racing both set it: harmless)
+template <auto kernel>
+hipError_t allow_lds(size_t lds) {
+    static std::atomic<uint64_t> set{0};
+    if (lds <= 65536) return hipSuccess;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev >= 64) return hipErrorInvalidDevice;
+    if (set.load(std::memory_order_relaxed) >> dev & 1) return hipSuccess;
+    const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             160 * 1024);
+    if (e == hipSuccess) set.fetch_or(uint64_t{1} << dev, std::memory_order_relaxed);
+    return e;
+}
+
 template <int BITS, int SBT, int MT, int T, int WPB>
 hipError_t launch_t(const QmmArgs& a) {
     constexpr int NMT = MT >= 4 ? MT / 4 : 1;
     const int blocks = (int)((a.N + 16 * T - 1) / (16 * T));
-    const size_t lds = sizeof(float) * WPB * T * 64 * NMT;
     const int gs_shift = __builtin_ctz((unsigned)a.group_size);
+    int sbl = 0;
+    const size_t lds = mfma_lds(a, T, WPB, NMT, &sbl);
+    const hipError_t e = allow_lds<qmv_mfma_kernel<BITS, SBT, MT, T, WPB>>(lds);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((qmv_mfma_kernel<BITS, SBT, MT, T, WPB>), dim3(blocks), dim3(WPB * 64), lds, a.stream,
                        (const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y,
-                       a.bias, (int)a.M, (int)a.N, (int)a.K, gs_shift, a.y_dtype);
+                       a.bias, (int)a.M, (int)a.N, (int)a.K, gs_shift, a.y_dtype, sbl);
     return hipGetLastError();
 }
 
@@ -360,11 +444,14 @@ template <int BITS, int SBT, int T, int WPB>
 hipError_t launch_gather_t(const QmmArgs& a, const MfmaGather& g, int64_t max_tiles) {
     constexpr int MT = kGatherGemvRows, NMT = MT / 4;
     const dim3 grid((unsigned)((a.N + 16 * T - 1) / (16 * T)), (unsigned)max_tiles);
-    const size_t lds = sizeof(float) * WPB * T * 64 * NMT;
     const int gs_shift = __builtin_ctz((unsigned)a.group_size);
+    int sbl = 0;
+    const size_t lds = mfma_lds(a, T, WPB, NMT, &sbl);
+    const hipError_t e = allow_lds<qmv_mfma_kernel<BITS, SBT, MT, T, WPB, true>>(lds);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((qmv_mfma_kernel<BITS, SBT, MT, T, WPB, true>), grid, dim3(WPB * 64), lds, a.stream,
                        (const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y,
-                       nullptr, MT, (int)a.N, (int)a.K, gs_shift, a.y_dtype, g);
+                       nullptr, MT, (int)a.N, (int)a.K, gs_shift, a.y_dtype, sbl, g);
     return hipGetLastError();
 }
 

@@ -61,10 +61,6 @@ constexpr int kSliceBytes = 1024;  // codes per K-slice: 64 lanes x 16 bytes
 #endif
 typedef __attribute__((ext_vector_type(2))) _Float16 half2_t;
 
-// s_waitcnt immediate: vmcnt(n), expcnt and lgkmcnt left unconstrained
-constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
-typedef __attribute__((address_space(3))) void lds_void;
 
 struct QmvsArgs {
     const uint16_t* x;

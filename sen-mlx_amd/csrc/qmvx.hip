@@ -42,8 +42,6 @@
 namespace miqmm {
 namespace {
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 constexpr int kMaxXElems = 32768;  // MT * K bf16 of x held in LDS (64 KiB)
 
 // s_waitcnt immediate for vmcnt(n) lgkmcnt(0) (vmcnt bits 3:0 and 15:14, expcnt 6:4 left at 7)
