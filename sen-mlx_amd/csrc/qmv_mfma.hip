@@ -75,12 +75,12 @@ __device__ __forceinline__ void transpose4x4(u32x4_t& v) {
     v[3] = d[1];
 }
 
-// group pairs per row that a wave stages (its k range, QS k-quads of 128
-// codes, starting at an even group), and the pairs of one array (scales or
-// biases) of a wave's LDS area: rows x pairs, rounded up to whole 64-lane
-// direct-to-LDS loads
-__host__ __device__ constexpr int sb_pairs(int K, int gs_shift, int wpb) {
-    return ((((K >> 5) + 3) >> 2) + wpb - 1) / wpb * (128 >> gs_shift) / 2 + 1;
+// group pairs per row that a wave stages: the whole group cycles (GS groups)
+// its k range (QS k-quads of 128 codes) touches, from an even group on; and
+// the pairs of one array (scales or biases) of a wave's LDS area: rows x
+// pairs, rounded up to whole 64-lane direct-to-LDS loads
+__host__ __device__ constexpr int sb_pairs(int K, int gs_shift, int wpb, int gs) {
+    return (((((K >> 5) + 3) >> 2) + wpb - 1) / wpb * (128 >> gs_shift) + 2 * gs + 1) / 2 + 1;
 }
 __host__ __device__ constexpr int sb_area_pairs(int T, int npr) { return (16 * T * npr + 63) / 64 * 64; }
 
@@ -109,14 +109,14 @@ __device__ __forceinline__ int sload(const int32_t* p) {  // wave-uniform scalar
     return __builtin_amdgcn_readfirstlane(*(const __attribute__((address_space(4))) int32_t*)p);
 }
 
-template <int BITS, int SBT, int MT, int T, int WPB, bool GATHER = false>
+template <int BITS, int SBT, int MT, int T, int WPB, bool GATHER, bool SBL>
 __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ w,
                                                             const uint16_t* __restrict__ sc,
                                                             const uint16_t* __restrict__ bi,
                                                             void* __restrict__ y,
                                                             const void* __restrict__ bias, int M, int N,
-                                                            int K, int gs_shift, int y_dtype, int sbl,
+                                                            int K, int gs_shift, int y_dtype,
                                                             const MfmaGather g = MfmaGather{}) {
     constexpr int GS = 16 / MT;                 // group slots per m
     constexpr int NMT = MT >= 4 ? MT / 4 : 1;   // distinct m per lane
@@ -125,6 +125,10 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
     // vector-memory loads of one stage: the codes (4-bit: one per tile;
     // 8-bit: two 8-byte loads per tile and register) and four x loads
     constexpr int kStageLoads = (BITS == 4 ? T : 4 * T) + 4;
+    // stages in flight (measured on MI355X, M = 16 on 4096 -> 14336: 26.3,
+    // 27.0 and 28.1 us with 2, 3 and 4)
+    constexpr int DEPTH = 2;
+    static_assert(DEPTH * kStageLoads < 64, "vmcnt range");
 
     extern __shared__ float red[];  // [WPB][T][64 lanes][NMT], then the waves' scale / bias areas
 
@@ -214,10 +218,11 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
     // GS < 4 only GS of them differ (r % GS = j % GS), so each distinct
     // scale / bias is loaded once (M = 16: one pair per row instead of four)
     constexpr int NG = GS < 4 ? GS : 4;
-    // this wave's LDS area: scales then biases, [16T rows][2 npr] halves of
-    // groups g0 .. g0 + 2 npr - 1 (g0 even), zero past G
-    const int npr = sb_pairs(K, gs_shift, WPB), area = sb_area_pairs(T, npr);
-    const int g0 = (u0 << (7 - gs_shift)) & ~1;
+    // this wave's LDS area (SBL): scales then biases, [16T rows][2 npr]
+    // halves of groups g0 .. g0 + 2 npr - 1, from the first group of its
+    // first cycle rounded down to even, zero past G
+    const int npr = sb_pairs(K, gs_shift, WPB, GS), area = sb_area_pairs(T, npr);
+    const int g0 = ((u0 << (7 - gs_shift)) / GS * GS) & ~1;
     uint16_t* const sl = reinterpret_cast<uint16_t*>(red + WPB * T * 64 * NMT) + wv * 4 * area;
     uint16_t* const bl = sl + 2 * area;
     auto rescale = [&](int c) {
@@ -229,12 +234,10 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
             for (int jj = 0; jj < NG; ++jj) {
                 const int g = c * GS + ((4 * q + jj) % GS);
                 uint16_t sh, bh;
-                if (sbl) {  // groups of the cycle outside this wave's range have no codes here: zero
-                    const int gi = g - g0;
-                    const bool in = g < G && gi >= 0 && gi < 2 * npr;
-                    const int li = in ? (int)row * 2 * npr + gi : 0;
-                    sh = in ? sl[li] : 0;
-                    bh = in ? bl[li] : 0;
+                if constexpr (SBL) {
+                    const int li = (int)row * 2 * npr + (g - g0);
+                    sh = sl[li];
+                    bh = bl[li];
                 } else {
                     const uint32_t off = g < G ? (row * G + g) * 2 : kOOB;
                     sh = bload2(sr, off);
@@ -293,12 +296,12 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
         }
     };
 
-    // one-deep pipeline over k-quads, ping-ponging two stages.  Each stage is
+    // pipeline over k-quads, DEPTH stages in flight.  Each stage is
     // refilled right after it is computed, unconditionally: a conditional
     // issue makes the compiler's wait before each compute count from the path
     // without the loads, i.e. wait for the stage just issued.
     if (u0 < u1) {
-        if (sbl) {  // stage the scales and biases, ahead of the stages' loads
+        if constexpr (SBL) {  // stage the scales and biases, ahead of the stages' loads
             const int npairs = 16 * T * npr;
             for (int d = 0; d * 64 < npairs; ++d) {
                 const int e = d * 64 + lane;
@@ -308,23 +311,26 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(br, (lds_void*)(bl + 128 * d), 4, off, 0, 0, 0);
             }
         }
-        St A, B;
-        issue(u0, A);
-        issue(u0 + 1, B);
+        St S[DEPTH];
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) issue(u0 + i, S[i]);
         // the staged scales land before any cycle reads them (the compiler
         // does not see that dependency): issued after them and still allowed
-        // in flight are the two stages' loads
+        // in flight are the stages' loads
         asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kStageLoads));
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(DEPTH * kStageLoads));
         asm volatile("" ::: "memory");
         int u = u0;
-        for (; u + 2 <= u1; u += 2) {
-            compute(u, A);
-            issue(u + 2, A);
-            compute(u + 1, B);
-            issue(u + 3, B);
+        for (; u + DEPTH <= u1; u += DEPTH) {
+#pragma unroll
+            for (int i = 0; i < DEPTH; ++i) {
+                compute(u + i, S[i]);
+                issue(u + i + DEPTH, S[i]);
+            }
         }
-        if (u < u1) compute(u, A);
+#pragma unroll
+        for (int i = 0; i + 1 < DEPTH; ++i)
+            if (u + i < u1) compute(u + i, S[i]);
         // a slice that ends mid-cycle has partial sums left in D
         const int last = min(4 * u1, KB) - 1;
         if (((last + 1) >> cl_shift) == (last >> cl_shift) && last + 1 != KB) rescale(last >> cl_shift);
@@ -362,9 +368,9 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
 // LDS of a launch: the cross-wave reduction, and the waves' scale / bias
 // areas when they stage them (an even number of groups per row, 4-byte
 // aligned arrays: the copies move group pairs; and room in the 160 KiB)
-size_t mfma_lds(const QmmArgs& a, int T, int wpb, int nmt, int* sbl) {
+size_t mfma_lds(const QmmArgs& a, int T, int wpb, int mt, int nmt, int* sbl) {
     const size_t red = sizeof(float) * wpb * T * 64 * nmt;
-    const int npr = sb_pairs((int)a.K, __builtin_ctz((unsigned)a.group_size), wpb);
+    const int npr = sb_pairs((int)a.K, __builtin_ctz((unsigned)a.group_size), wpb, 16 / mt);
     const size_t stage = (size_t)wpb * 2 * sb_area_pairs(T, npr) * 4;
     const bool al = ((reinterpret_cast<uintptr_t>(a.scales) | reinterpret_cast<uintptr_t>(a.biases)) & 3) == 0;
     *sbl = (a.K / a.group_size) % 2 == 0 && al && red + stage <= 160 * 1024 ? 1 : 0;
@@ -385,49 +391,60 @@ hipError_t allow_lds(size_t lds) {
     return e;
 }
 
+template <int BITS, int SBT, int MT, int T, int WPB, bool GATHER, bool SBL>
+hipError_t launch_k(const QmmArgs& a, dim3 grid, size_t lds, const MfmaGather& g) {
+    const hipError_t e = allow_lds<qmv_mfma_kernel<BITS, SBT, MT, T, WPB, GATHER, SBL>>(lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((qmv_mfma_kernel<BITS, SBT, MT, T, WPB, GATHER, SBL>), grid, dim3(WPB * 64), lds, a.stream,
+                       (const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y,
+                       GATHER ? nullptr : a.bias, GATHER ? MT : (int)a.M, (int)a.N, (int)a.K,
+                       __builtin_ctz((unsigned)a.group_size), a.y_dtype, g);
+    return hipGetLastError();
+}
+
 template <int BITS, int SBT, int MT, int T, int WPB>
 hipError_t launch_t(const QmmArgs& a) {
     constexpr int NMT = MT >= 4 ? MT / 4 : 1;
-    const int blocks = (int)((a.N + 16 * T - 1) / (16 * T));
-    const int gs_shift = __builtin_ctz((unsigned)a.group_size);
+    const dim3 grid((unsigned)((a.N + 16 * T - 1) / (16 * T)));
     int sbl = 0;
-    const size_t lds = mfma_lds(a, T, WPB, NMT, &sbl);
-    const hipError_t e = allow_lds<qmv_mfma_kernel<BITS, SBT, MT, T, WPB>>(lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((qmv_mfma_kernel<BITS, SBT, MT, T, WPB>), dim3(blocks), dim3(WPB * 64), lds, a.stream,
-                       (const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y,
-                       a.bias, (int)a.M, (int)a.N, (int)a.K, gs_shift, a.y_dtype, sbl);
-    return hipGetLastError();
+    const size_t lds = mfma_lds(a, T, WPB, MT, NMT, &sbl);
+    return sbl ? launch_k<BITS, SBT, MT, T, WPB, false, true>(a, grid, lds, MfmaGather{})
+               : launch_k<BITS, SBT, MT, T, WPB, false, false>(a, grid, lds, MfmaGather{});
 }
 
 int pick_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
 // tiles per block and waves per block: 16 K-splitting waves once K has at
-// least 64 k-quads (K >= 8192), else 4; then the most 16-row tiles per block
-// (4, 2 or 1: more tiles amortise the x operand, which every block reads
-// whole from L2) that still give 192 blocks, three quarters of the CUs.
-// Measured on MI355X (4-bit g64, M = 8 / 16): 4096 -> 14336 30.2 / 40.6
-// -> 26.8 / 32.0 us, 14336 -> 4096 45.3 / 53.3 -> 29.6 / 37.0 us, 4096 ->
-// 4096 17.7 / 20.8 -> 12.0 / 15.5 us against the earlier choice (16 waves from
-// K = 2048, four tiles unless too few waves in flight); then 192 blocks
-// instead of 256: 4096 -> 14336 at M = 8 26.3 -> 25.2 us, 4096 -> 6144
-// 16.2 / 21.3 -> 15.7 / 19.7 us, the rest unchanged (128 blocks: 4096 ->
-// 4096 at M = 16 15.5 -> 19.4 us).
+// least 64 k-quads (K >= 8192) and M <= 8, else 4; then the most 16-row
+// tiles per block (4, 2 or 1: more tiles amortise the x operand, which every
+// block reads whole from L2) that still give 192 blocks, three quarters of
+// the CUs.  Measured on MI355X with the scales staged in LDS (4-bit g64, us,
+// M = 8 / 16; the choice first): 4096 -> 14336 (T 4) 15.7 / 19.1, T 2 14.9 /
+// 18.9, T 1 18.0 / 23.6; 14336 -> 4096 (T 1, 16 waves) 18.2 / 24.5, four
+// waves 22.4 / 20.6 (hence four at M = 16), T 2 with 16 waves 23.8 / 30.0;
+// 4096 -> 4096 (T 1) 9.1 / 8.9, T 2 10.9 / 11.8.
 void pick_tw(int64_t M, int64_t N, int64_t K, int bits, int* T, int* WPB) {
     const int64_t KQ = (K / 32 + 3) / 4;
     const int nmt = M > 4 ? (M > 8 ? 4 : 2) : 1;
-    const int wpb = KQ >= 64 ? 16 : 4;
+    const int wpb = KQ >= 64 && M <= 8 ? 16 : 4;
     int t = 4;
     while (t > 1 && (N + 16 * t - 1) / (16 * t) < 192) t /= 2;
     while (t > 1 && wpb * t * 64 * nmt * 4 > 32768) t /= 2;  // cross-wave reduction LDS
-    if (bits == 8 && wpb == 16 && t > 2) t = 2;  // 8-bit stages need the registers of two tiles
+    // 16 waves of a block get at most 128 registers each: four tiles' stages
+    // and accumulators do not fit in them (they spilled)
+    if (wpb == 16 && t > 2) t = 2;
+    (void)bits;
     *T = t;
     *WPB = wpb;
 }
 
 template <int BITS, int SBT, int MT, int T>
 hipError_t launch_w(const QmmArgs& a, int wpb) {
-    return wpb == 16 ? launch_t<BITS, SBT, MT, T, 16>(a) : launch_t<BITS, SBT, MT, T, 4>(a);
+    if constexpr (T == 4) {  // four waves only (pick_tw)
+        return launch_t<BITS, SBT, MT, T, 4>(a);
+    } else {
+        return wpb == 16 ? launch_t<BITS, SBT, MT, T, 16>(a) : launch_t<BITS, SBT, MT, T, 4>(a);
+    }
 }
 
 template <int BITS, int SBT, int MT>
@@ -444,15 +461,10 @@ template <int BITS, int SBT, int T, int WPB>
 hipError_t launch_gather_t(const QmmArgs& a, const MfmaGather& g, int64_t max_tiles) {
     constexpr int MT = kGatherGemvRows, NMT = MT / 4;
     const dim3 grid((unsigned)((a.N + 16 * T - 1) / (16 * T)), (unsigned)max_tiles);
-    const int gs_shift = __builtin_ctz((unsigned)a.group_size);
     int sbl = 0;
-    const size_t lds = mfma_lds(a, T, WPB, NMT, &sbl);
-    const hipError_t e = allow_lds<qmv_mfma_kernel<BITS, SBT, MT, T, WPB, true>>(lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((qmv_mfma_kernel<BITS, SBT, MT, T, WPB, true>), grid, dim3(WPB * 64), lds, a.stream,
-                       (const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y,
-                       nullptr, MT, (int)a.N, (int)a.K, gs_shift, a.y_dtype, sbl, g);
-    return hipGetLastError();
+    const size_t lds = mfma_lds(a, T, WPB, MT, NMT, &sbl);
+    return sbl ? launch_k<BITS, SBT, MT, T, WPB, true, true>(a, grid, lds, g)
+               : launch_k<BITS, SBT, MT, T, WPB, true, false>(a, grid, lds, g);
 }
 
 template <int BITS, int SBT>
