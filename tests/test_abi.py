@@ -242,7 +242,9 @@ def test_query_route(lib):
         assert route == miqmm.ROUTE_QMM and tiles == (256, bn, 64, ks), ((M, N, K), tiles)
     # the MFMA GEMV's launch shape: the most tiles per block that still give 192 blocks
     assert miqmm.query_route(8, 14336, 4096, 64, 4)[1] == (4, 8, 4, 0)  # 224 blocks of four tiles
-    assert miqmm.query_route(16, 4096, 14336, 64, 4)[1] == (1, 16, 16, 0)
+    # K >= 8192: sixteen K-splitting waves at M <= 8, four at M = 16
+    assert miqmm.query_route(8, 4096, 14336, 64, 4)[1] == (1, 8, 16, 0)
+    assert miqmm.query_route(16, 4096, 14336, 64, 4)[1] == (1, 16, 4, 0)
     with pytest.raises(miqmm.MiqmmError) as e:
         miqmm.query_route(1, 64, 96, 64, 4)
     assert e.value.status == miqmm.EINVAL
