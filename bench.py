@@ -447,7 +447,10 @@ def step_types(miqmm, torch):
         r = line(sec, nb)
         r["launches_per_step"] = count
         r["us_per_step"] = round(sec * 1e6 * count, 2)
-        r["route"] = miqmm.query_route(1, Ns[0], K, 64, 4)[0] if len(Ns) == 1 else "grouped v_dot2, contiguous"
+        # a contiguous group runs as one matrix of all its rows
+        r["route"] = miqmm.query_route(1, sum(Ns), K, 64, 4)[0]
+        if len(Ns) > 1:
+            r["grouped"] = "contiguous, one launch"
         res[name] = r
         torch.cuda.empty_cache()
     return res

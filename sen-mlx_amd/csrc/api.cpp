@@ -102,19 +102,27 @@ int check_launch(hipError_t e, const char* what) {
 }
 
 // Rows of at least this many codes take the K-sliced GEMV at M = 1 (one
-// wave per 1 KiB slice of codes; shorter rows would leave most lanes idle)
+// wave per 1 KiB slice of codes); so do rows of at most 32 16-byte chunks
+// (the half-wave rows, two rows per wave slice).  Rows in between would
+// leave a quarter to half of the lanes idle and keep the v_dot2 GEMV.
 constexpr int64_t kMinSlicedK = 2048;
+bool short_rows(int64_t K, int bits) { return K * bits / 128 <= 32; }
 
 // Measured on MI355X (4-bit g64, cold weights):
-//   M = 1, K >= 2048: the K-sliced GEMV (4096 -> 14336: 7.9 us against 9.2 us);
-//   M = 1, shorter rows: the v_dot2 GEMV, except for many-row, short-K heads (lm_head 896 ->
-//          151936: 18.8 us against 22.8 us), where the LDS-staged MFMA GEMV wins;
+//   M = 1, K >= 2048: the K-sliced GEMV (4096 -> 14336: 7.8 us against 8.6 us);
+//   M = 1, rows of at most 32 chunks: the K-sliced GEMV on half-wave rows
+//          (896 -> 896 2.34 us against 2.51; 896 -> 9728 3.23 against 3.43;
+//          the 896 -> 151936 head 14.3 us against 17.9 for the LDS-staged
+//          MFMA GEMV and 19.3 for v_dot2);
+//   M = 1, other rows: the v_dot2 GEMV, except for many-row heads with K <=
+//          2048, where the LDS-staged MFMA GEMV wins;
 //   2 <= M <= 4: the LDS-staged MFMA GEMV (14336 x 4096: 12.8 / 16.0 us at
 //          M = 2 / 4 against 15.1 / 22.2 us for v_dot2) when it supports the shape;
 //   5 <= M <= 16: the group-diagonal MFMA GEMV, whose cost barely grows with M;
 //   larger M: the tiled MFMA matmul.
 int auto_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, bool sb_aligned4 = true) {
-    if (M == 1 && K >= kMinSlicedK && sb_aligned4 && miqmm::qmvs_supported(M, N, K, bits, group_size))
+    if (M == 1 && (K >= kMinSlicedK || short_rows(K, bits)) && sb_aligned4 &&
+        miqmm::qmvs_supported(M, N, K, bits, group_size))
         return MIQMM_ROUTE_QMVS;
     if (M == 1) {
         const bool wide_head = N >= 65536 && K <= 2048 && miqmm::qmvx_supported(M, K, group_size);
@@ -340,14 +348,13 @@ int miqmm_quantized_matmul_ws(void* y, const void* x, const uint32_t* w, const v
                       y_dtype, MIQMM_ROUTE_AUTO, stream, workspace, workspace ? workspace_bytes : 0);
 }
 
-
-
 int miqmm_quantized_matmul_grouped(const miqmm_problem* problems, int count, int64_t M, int64_t K,
                                    int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
                                    void* stream) {
     if (count < 0 || (count > 0 && !problems)) return fail(MIQMM_EINVAL, "problems must hold count >= 0 entries");
     // decode-sized projections (M <= 2, none of them a wide head) run as one
-    // grouped v_dot2 GEMV launch per four: at these sizes the launches are
+    // grouped GEMV launch per four (the K-sliced GEMV when they are stored
+    // contiguously, else the v_dot2 GEMV): at these sizes the launches are
     // latency-bound, so fewer of them beat a faster per-shape route
     bool grouped = M >= 1 && M <= 2;
     for (int i = 0; i < count; ++i) {
@@ -368,10 +375,22 @@ int miqmm_quantized_matmul_grouped(const miqmm_problem* problems, int count, int
         }
         return ok();
     }
+    miqmm::QmmArgs a[miqmm::kMaxGroup];
+    // one row of x and problems stored one after another (fused at load),
+    // with rows the K-sliced GEMV takes: one launch over all their rows
+    if (M == 1 && count <= miqmm::kMaxGroup && (K >= kMinSlicedK || short_rows(K, bits)) &&
+        aligned4(problems[0].scales) && aligned4(problems[0].biases)) {
+        for (int i = 0; i < count; ++i) {
+            const miqmm_problem& p = problems[i];
+            a[i] = miqmm::QmmArgs{p.y, p.x, p.w, p.scales, p.biases, p.bias, M, p.N, K, group_size, bits,
+                                  x_dtype, sb_dtype, y_dtype, reinterpret_cast<hipStream_t>(stream)};
+        }
+        if (miqmm::qmvs_group_ok(a, count))
+            return check_launch(miqmm::launch_qmvs_grouped(a, count), "grouped qmvs launch");
+    }
     // a problem that the GEMV alone would run with K split over a block's
     // waves is launched alone, so that every result equals the v_dot2 route
     // on that problem bit for bit (the split changes the order of the sums)
-    miqmm::QmmArgs a[miqmm::kMaxGroup];
     int n = 0;
     for (int i = 0; i <= count; ++i) {
         if (i < count) {

@@ -94,6 +94,12 @@ hipError_t launch_qmvs(const QmmArgs& a);      // K-sliced v_dot2 GEMV, M == 1
 // M == 1, at most 15 K-slices, an even number of groups per row (the scale
 // and bias pointers must also be 4-byte aligned, checked by the caller)
 bool qmvs_supported(int64_t M, int64_t N, int64_t K, int bits, int group_size);
+// a[0..count) (2..4 problems, M == 1) share x and store their codes, scales
+// and biases one after another (a loader that fuses q/k/v or gate/up): the
+// K-sliced GEMV reads them as one matrix and writes each problem's rows to
+// its own output
+bool qmvs_group_ok(const QmmArgs* a, int count);
+hipError_t launch_qmvs_grouped(const QmmArgs* a, int count);
 // compute units of the current device (queried once per device): the GEMV
 // grids are sized by it
 int num_cus();

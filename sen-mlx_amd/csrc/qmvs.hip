@@ -38,6 +38,7 @@
 // M = 1, 4096 -> 14336 and 14336 -> 4096 in 7.9 us (4.2 TB/s) against 9.2 and
 // 9.9 us for the v_dot2 GEMV; the 5376 -> 262144 head in 113 us (7.0 TB/s);
 // a bare streaming read of the same 33 MB takes 5.9 us.
+#include <climits>
 #include <type_traits>
 
 #include "miqmm_device.h"
@@ -48,11 +49,6 @@ namespace {
 
 constexpr int kSliceBytes = 1024;  // codes per K-slice: 64 lanes x 16 bytes
 
-// cache policy of the output stores (0: default; measured on MI355X, a
-// non-temporal store per block added 3.5 us to a 6 us streaming read)
-#ifndef QMVS_STORE_POLICY
-#define QMVS_STORE_POLICY 0
-#endif
 
 // fp16 operands for the 4-bit unpack (codes at bits 0-3 and 4-7 of each
 // half are exact fp16 mantissas, one shift per word fewer than bf16)
@@ -70,6 +66,16 @@ struct QmvsArgs {
     void* y;
     const void* bias;
     int N, K, gs_shift, y_dtype;
+};
+
+// Problems 1..3 of a contiguous group: their codes, scales and biases
+// follow problem 0's (the kernel reads one matrix of all their rows); row0
+// is each one's first row in it (unused: INT_MAX) and y / bias its output
+// and bias.  Problem 0's are the kernel's own y and bias.
+struct QmvsGroup {
+    void* y[3];
+    const void* bias[3];
+    int row0[3];
 };
 
 // LDS per wave: scales then biases of its rows, ND KiB each (a direct-to-LDS
@@ -91,17 +97,13 @@ __device__ __forceinline__ float dpp(float v) {
 // sum of value l >> (6 - log2 RB): lanes 64/RB * j .. of row j.  About
 // 3 RB instructions for the RB values, against 12 per value for one
 // butterfly per value.
+// From the state after the first exchange: H = RB / 2 values per lane,
+// lanes 0-31 holding values j and lanes 32-63 values j + H (also the state
+// of a wave whose two halves compute different rows).
 template <int RB>
-__device__ __forceinline__ float transposed_sum(float (&v)[RB], int lane) {
+__device__ __forceinline__ float transposed_sum32(const float (&b)[RB / 2], int lane) {
     static_assert(RB == 4 || RB == 8 || RB == 16 || RB == 32, "rows per reduction");
     constexpr int H = RB / 2;
-    float b[H];
-#pragma unroll
-    for (int j = 0; j < H; ++j) {  // lanes 0-31: value j, lanes 32-63: value j + H
-        const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + H]), false,
-                                                        false);
-        b[j] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
-    }
     constexpr int Q = H / 2;
     float c[Q];
 #pragma unroll
@@ -158,6 +160,19 @@ __device__ __forceinline__ float transposed_sum(float (&v)[RB], int lane) {
     return r;
 }
 
+template <int RB>
+__device__ __forceinline__ float transposed_sum(const float (&v)[RB], int lane) {
+    constexpr int H = RB / 2;
+    float b[H];
+#pragma unroll
+    for (int j = 0; j < H; ++j) {  // lanes 0-31: value j, lanes 32-63: value j + H
+        const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + H]), false,
+                                                        false);
+        b[j] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+    }
+    return transposed_sum32<RB>(b, lane);
+}
+
 // RB rows per block; ND direct-to-LDS loads per scale (and bias) array:
 // RB * (bytes of scales per row and slice) / 1 KiB, rounded up
 template <int RB>
@@ -168,10 +183,16 @@ constexpr int max_threads() { return RB >= 32 ? 512 : 1024; }  // 32 rows of cod
 // the scalar memory round trip before the first load (bias, read last, is
 // past the preloaded registers).  meta = log2 group size | y dtype << 8 |
 // waves per block << 16 (blockDim would be a load of the implicit arguments).
-template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS>
+//
+// HALF (rows of at most 32 chunks, one slice): the wave's halves compute
+// different rows, lanes 32h .. 32h + 31 the rows h RB/2 .. h RB/2 + RB/2 - 1
+// of the block, so no lane idles past a short row's end (K = 896 at 4 bits
+// is 28 chunks); the reduction starts from its 32-lane state.
+template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF>
 __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t* xp, const uint32_t* wp,
                                                                  const uint16_t* sp, const uint16_t* bp, int n, int k,
-                                                                 uint32_t meta, void* yp, const void* biasp) {
+                                                                 uint32_t meta, void* yp, const void* biasp,
+                                                                 const QmvsGroup grp) {
     const QmvsArgs P{xp, wp, sp, bp, yp, biasp, n, k, (int)(meta & 0xff), (int)((meta >> 8) & 0xff)};
     constexpr int CPC_SHIFT = BITS == 4 ? 5 : 4;  // codes per 16-byte chunk: 32 or 16
     constexpr int CPC = 1 << CPC_SHIFT;
@@ -184,7 +205,10 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     const int KS = (int)(meta >> 16);
     const int K = P.K, gs_shift = P.gs_shift;
     const int C = K >> CPC_SHIFT;       // chunks per row
-    const int c = ws * 64 + lane;       // this lane's chunk of every row
+    constexpr int RL = HALF ? RB / 2 : RB;          // rows per lane
+    const int lc = HALF ? lane & 31 : lane;          // this lane's chunk within the slice
+    const int rh = HALF ? (lane >> 5) * RL : 0;      // first of this lane's rows in the block
+    const int c = ws * 64 + lc;         // this lane's chunk of every row
     const bool cv = c < C;
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
@@ -234,18 +258,23 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     __builtin_amdgcn_sched_barrier(0);
     // codes of the block's rows (rows past the block's last read zero)
     const auto wr = make_rsrc((const char*)P.w + (size_t)r0 * row_bytes, (uint32_t)nrows * row_bytes);
-    u32x4_t q[RB];
+    u32x4_t q[RL];
 #pragma unroll
-    for (int j = 0; j < RB; ++j) q[j] = bload16_nt(wr, cv ? (uint32_t)j * row_bytes + (uint32_t)c * 16 : kOOB);
-    // the bias of the row this lane stores: row t of the block by lane t of wave 0
+    for (int j = 0; j < RL; ++j)
+        q[j] = bload16_nt(wr, cv ? (uint32_t)(rh + j) * row_bytes + (uint32_t)c * 16 : kOOB);
+    // the row this lane stores: row t of the block by lane t of wave 0, into
+    // its problem's output (and with its bias)
     const int t_row = lane;
     const bool t_mine = ws == 0 && lane < nrows;
+    const int t_glob = r0 + t_row;
+    const int t_p = (t_glob >= grp.row0[0]) + (t_glob >= grp.row0[1]) + (t_glob >= grp.row0[2]);
+    const size_t t_off = (size_t)(t_glob - (t_p == 0 ? 0 : grp.row0[t_p - 1])) * ysz;
     uint32_t bias_bits = 0;
-    if constexpr (BIAS) {
-        const auto biasr = make_rsrc((const char*)P.bias + (size_t)r0 * ysz, (uint32_t)nrows * ysz);
-        const uint32_t boff = t_mine ? (uint32_t)t_row * ysz : kOOB;
-        if constexpr (YF32) bias_bits = __builtin_amdgcn_raw_buffer_load_b32(biasr, boff, 0, 0);
-        else bias_bits = __builtin_amdgcn_raw_buffer_load_b16(biasr, boff, 0, 0);
+    if constexpr (BIAS) {  // every lane loads (a lane past the rows reads row 0's): one load, counted below
+        const char* const bp0 = t_p == 0 ? (const char*)P.bias : (const char*)grp.bias[t_p - 1];
+        const char* const ba = t_mine ? bp0 + t_off : (const char*)P.bias;
+        if constexpr (YF32) bias_bits = *reinterpret_cast<const uint32_t*>(ba);
+        else bias_bits = *reinterpret_cast<const uint16_t*>(ba);
     }
 
     __builtin_amdgcn_sched_barrier(0);
@@ -300,7 +329,7 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     // not track that dependency): issued after it and still allowed in
     // flight are the codes (and the bias)
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(RB + (BIAS ? 1 : 0)));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(RL + (BIAS ? 1 : 0)));
     asm volatile("" ::: "memory");
 
     const uint32_t kMask = vgpr_const(0x000F000Fu), kMagic = kMagic128x2;
@@ -308,19 +337,20 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     const uint32_t kMaskHi = vgpr_const(0x00F000F0u);
 #endif
     // this lane's scale / bias of row j at j * sb + 2 * (group in slice)
-    const uint32_t sl_off = (uint32_t)((lane << CPC_SHIFT) >> gs_shift) * 2;
+    const uint32_t sl_off = (uint32_t)((lc << CPC_SHIFT) >> gs_shift) * 2;
     // per-lane partial of every row; in the wave of the slice that runs past
     // the row end (if any), lanes past it take zero scales and biases, so
     // they add nothing whatever their LDS holds
     const bool partial = __builtin_amdgcn_readfirstlane((int)(ws == KS - 1 && (C & 63) != 0)) != 0;
-    float part[RB];
+    float part[RL];
     auto rows = [&](auto masked) {
 #pragma unroll
-        for (int j = 0; j < RB; ++j) {
+        for (int j = 0; j < RL; ++j) {
             uint32_t p[NP];
             float a = 0.f;
-            float s = half_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(wl + j * sb + sl_off));
-            float b = half_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(wl + ND * kSliceBytes + j * sb + sl_off));
+            const int jr = rh + j;  // row of the block
+            float s = half_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(wl + jr * sb + sl_off));
+            float b = half_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(wl + ND * kSliceBytes + jr * sb + sl_off));
             if constexpr (decltype(masked)::value) {
                 s = cv ? s : 0.f;
                 b = cv ? b : 0.f;
@@ -358,7 +388,9 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     (void)partial;
     rows(std::true_type{});
     // the wave's sum of row j lands in lanes (64 / RB) j .. (64 / RB) (j + 1) - 1
-    const float tot = transposed_sum<RB>(part, lane);
+    float tot;
+    if constexpr (HALF) tot = transposed_sum32<RB>(part, lane);
+    else tot = transposed_sum<RB>(part, lane);
     // the slice partials meet in LDS; row t is summed (slices in order) and
     // stored by lane t of wave 0
     float* const kp = reinterpret_cast<float*>(smem + KS * wave_lds<ND>());
@@ -370,11 +402,12 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     if (!t_mine) return;
     float v = 0.f;
     for (int w = 0; w < KS; ++w) v += kp[w * RB + t_row];
-    const auto yr = make_rsrc((char*)P.y + (size_t)r0 * ysz, (uint32_t)nrows * ysz);
-    const uint32_t yoff = (uint32_t)t_row * ysz;
+    // plain stores (measured on MI355X: a non-temporal store per block added
+    // 3.5 us to a 6 us streaming read)
+    char* const ya = (t_p == 0 ? (char*)P.y : (char*)grp.y[t_p - 1]) + t_off;
     if constexpr (YF32) {
         if constexpr (BIAS) v += __uint_as_float(bias_bits);
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yr, yoff, 0, QMVS_STORE_POLICY);
+        *reinterpret_cast<float*>(ya) = v;
     } else {
         // rounded to y's dtype, then the bias added and rounded again (two MLX ops)
         uint16_t h;
@@ -385,7 +418,7 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
             h = f32_to_bf16_bits(v);
             if constexpr (BIAS) h = f32_to_bf16_bits(bf16_bits_to_f32(h) + bf16_bits_to_f32(bias_bits));
         }
-        __builtin_amdgcn_raw_buffer_store_b16(h, yr, yoff, 0, QMVS_STORE_POLICY);
+        *reinterpret_cast<uint16_t*>(ya) = h;
     }
 }
 
@@ -408,42 +441,58 @@ int rows_per_block(int64_t N, int ks) {
     return 4;
 }
 
-template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS>
-hipError_t launch_t(const QmmArgs& a, int ks) {
+template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF>
+hipError_t launch_t(const QmmArgs& a, const QmvsGroup& g, int ks) {
     const QmvsArgs P{(const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y, a.bias,
                      (int)a.N, (int)a.K, __builtin_ctz((unsigned)a.group_size), a.y_dtype};
     const size_t lds = (size_t)ks * wave_lds<ND>() + (size_t)ks * RB * 4;
     const int blocks = (int)((a.N + RB - 1) / RB);
-    hipLaunchKernelGGL((qmvs_kernel<BITS, SBT, RB, ND, YF32, BIAS>), dim3(blocks), dim3(64 * ks), lds, a.stream, P.x,
-                       P.w, P.s, P.b, P.N, P.K, (uint32_t)P.gs_shift | (uint32_t)P.y_dtype << 8 | (uint32_t)ks << 16, P.y, P.bias);
+    hipLaunchKernelGGL((qmvs_kernel<BITS, SBT, RB, ND, YF32, BIAS, HALF>), dim3(blocks), dim3(64 * ks), lds, a.stream, P.x,
+                       P.w, P.s, P.b, P.N, P.K, (uint32_t)P.gs_shift | (uint32_t)P.y_dtype << 8 | (uint32_t)ks << 16, P.y,
+                       P.bias, g);
     return hipGetLastError();
 }
 
+// rows of at most 32 chunks in one slice: the half-wave rows
+bool half_rows(int64_t K, int bits) { return slices(K, bits) == 1 && K * bits / 128 <= 32; }
+
+template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS>
+hipError_t launch_h(const QmmArgs& a, const QmvsGroup& g, int ks) {
+    return half_rows(a.K, BITS) ? launch_t<BITS, SBT, RB, ND, YF32, BIAS, true>(a, g, ks)
+                                : launch_t<BITS, SBT, RB, ND, YF32, BIAS, false>(a, g, ks);
+}
+
 template <int BITS, int SBT, int RB, bool YF32, bool BIAS>
-hipError_t launch_nd(const QmmArgs& a, int ks) {
+hipError_t launch_nd(const QmmArgs& a, const QmvsGroup& g, int ks) {
     // bytes of scales per row and slice: (1 KiB of codes / group) * 2
     const int sb = 2 * ((kSliceBytes * 8 / BITS) / a.group_size);
-    if (RB * sb > 2 * kSliceBytes) return launch_t<BITS, SBT, RB, 4, YF32, BIAS>(a, ks);
-    if (RB * sb > kSliceBytes) return launch_t<BITS, SBT, RB, 2, YF32, BIAS>(a, ks);
-    return launch_t<BITS, SBT, RB, 1, YF32, BIAS>(a, ks);
+    if (RB * sb > 2 * kSliceBytes) return launch_h<BITS, SBT, RB, 4, YF32, BIAS>(a, g, ks);
+    if (RB * sb > kSliceBytes) return launch_h<BITS, SBT, RB, 2, YF32, BIAS>(a, g, ks);
+    return launch_h<BITS, SBT, RB, 1, YF32, BIAS>(a, g, ks);
 }
 
 template <int BITS, int SBT, bool YF32, bool BIAS>
-hipError_t launch_rb(const QmmArgs& a) {
+hipError_t launch_rb(const QmmArgs& a, const QmvsGroup& g) {
     const int ks = slices(a.K, BITS);
     switch (rows_per_block(a.N, ks)) {
-        case 32: return launch_nd<BITS, SBT, 32, YF32, BIAS>(a, ks);
-        case 16: return launch_nd<BITS, SBT, 16, YF32, BIAS>(a, ks);
-        case 8: return launch_nd<BITS, SBT, 8, YF32, BIAS>(a, ks);
-        default: return launch_nd<BITS, SBT, 4, YF32, BIAS>(a, ks);
+        case 32: return launch_nd<BITS, SBT, 32, YF32, BIAS>(a, g, ks);
+        case 16: return launch_nd<BITS, SBT, 16, YF32, BIAS>(a, g, ks);
+        case 8: return launch_nd<BITS, SBT, 8, YF32, BIAS>(a, g, ks);
+        default: return launch_nd<BITS, SBT, 4, YF32, BIAS>(a, g, ks);
     }
 }
 
 template <bool YF32, bool BIAS>
-hipError_t launch_y(const QmmArgs& a) {
+hipError_t launch_y(const QmmArgs& a, const QmvsGroup& g) {
     if (a.bits == 4)
-        return a.sb_dtype == DT_F16 ? launch_rb<4, DT_F16, YF32, BIAS>(a) : launch_rb<4, DT_BF16, YF32, BIAS>(a);
-    return a.sb_dtype == DT_F16 ? launch_rb<8, DT_F16, YF32, BIAS>(a) : launch_rb<8, DT_BF16, YF32, BIAS>(a);
+        return a.sb_dtype == DT_F16 ? launch_rb<4, DT_F16, YF32, BIAS>(a, g) : launch_rb<4, DT_BF16, YF32, BIAS>(a, g);
+    return a.sb_dtype == DT_F16 ? launch_rb<8, DT_F16, YF32, BIAS>(a, g) : launch_rb<8, DT_BF16, YF32, BIAS>(a, g);
+}
+
+hipError_t launch_g(const QmmArgs& a, const QmvsGroup& g) {
+    if (a.M != 1) return hipErrorInvalidValue;
+    if (a.y_dtype == DT_F32) return a.bias ? launch_y<true, true>(a, g) : launch_y<true, false>(a, g);
+    return a.bias ? launch_y<false, true>(a, g) : launch_y<false, false>(a, g);
 }
 
 }  // namespace
@@ -465,9 +514,38 @@ void qmvs_config(const QmmArgs& a, int* rows_per_blk, int* slices_out, int* bloc
 }
 
 hipError_t launch_qmvs(const QmmArgs& a) {
-    if (a.M != 1) return hipErrorInvalidValue;
-    if (a.y_dtype == DT_F32) return a.bias ? launch_y<true, true>(a) : launch_y<true, false>(a);
-    return a.bias ? launch_y<false, true>(a) : launch_y<false, false>(a);
+    const QmvsGroup g{{nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr}, {INT_MAX, INT_MAX, INT_MAX}};
+    return launch_g(a, g);
+}
+
+bool qmvs_group_ok(const QmmArgs* a, int count) {
+    if (count < 2 || count > 4 || a[0].M != 1) return false;
+    const int64_t row_bytes = a[0].K * a[0].bits / 8, sb_row = a[0].K / a[0].group_size * 2;
+    int64_t rows = 0;
+    for (int i = 0; i < count; ++i) {
+        if (a[i].x != a[0].x || (a[i].bias == nullptr) != (a[0].bias == nullptr)) return false;
+        if ((const char*)a[i].w != (const char*)a[0].w + rows * row_bytes) return false;
+        if ((const char*)a[i].scales != (const char*)a[0].scales + rows * sb_row) return false;
+        if ((const char*)a[i].biases != (const char*)a[0].biases + rows * sb_row) return false;
+        rows += a[i].N;
+    }
+    return rows < ((int64_t)1 << 31) && qmvs_supported(1, rows, a[0].K, a[0].bits, a[0].group_size);
+}
+
+hipError_t launch_qmvs_grouped(const QmmArgs* a, int count) {
+    if (!qmvs_group_ok(a, count)) return hipErrorInvalidValue;
+    QmvsGroup g{{nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr}, {INT_MAX, INT_MAX, INT_MAX}};
+    QmmArgs all = a[0];
+    all.N = 0;
+    for (int i = 0; i < count; ++i) {
+        if (i > 0) {
+            g.y[i - 1] = a[i].y;
+            g.bias[i - 1] = a[i].bias;
+            g.row0[i - 1] = (int)all.N;
+        }
+        all.N += a[i].N;
+    }
+    return launch_g(all, g);
 }
 
 }  // namespace miqmm

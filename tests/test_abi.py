@@ -218,12 +218,16 @@ def test_query_route(lib):
     assert miqmm.query_route(1, 262144, 5376, 64, 8) == (miqmm.ROUTE_QMVS, (16, 6, 16384, 0))
     # an odd number of groups per row keeps the v_dot2 GEMV (scale rows not 4-byte aligned)
     assert miqmm.query_route(1, 4096, 2080, 32, 4)[0] == miqmm.ROUTE_QMV_DOT
-    # shorter rows: the v_dot2 GEMV, lanes per row by chunk count
-    route, tiles = miqmm.query_route(1, 4864, 896, 64, 4)
-    assert route == miqmm.ROUTE_QMV_DOT and tiles[2] == 32  # 28 chunks per row -> 32 lanes
-    # wide, short-K head at M = 1 and 2 <= M <= 4: the LDS-staged MFMA GEMV (m tile, k-splits, codes per stage)
-    route, tiles = miqmm.query_route(1, 151936, 896, 64, 4)
-    assert route == miqmm.ROUTE_QMVX and tiles[:3] == (1, 1, 1024)
+    # rows of at most 32 chunks (K <= 1024 at 4 bits): the K-sliced GEMV, two
+    # rows per wave slice; 4 rows per block below ~3 waves per CU
+    assert miqmm.query_route(1, 4864, 896, 64, 4) == (miqmm.ROUTE_QMVS, (4, 1, 1216, 0))
+    assert miqmm.query_route(1, 151936, 896, 64, 4) == (miqmm.ROUTE_QMVS, (16, 1, 9496, 0))
+    # rows in between: the v_dot2 GEMV, lanes per row by chunk count
+    route, tiles = miqmm.query_route(1, 4864, 1536, 64, 4)
+    assert route == miqmm.ROUTE_QMV_DOT and tiles[2] == 16  # 48 chunks per row -> 16 lanes, no idle one
+    # 2 <= M <= 4: the LDS-staged MFMA GEMV (m tile, k-splits, codes per stage)
+    route, tiles = miqmm.query_route(2, 151936, 896, 64, 4)
+    assert route == miqmm.ROUTE_QMVX and tiles[0] == 2
     for M, mt in ((2, 2), (3, 4), (4, 4)):
         route, tiles = miqmm.query_route(M, 14336, 4096, 64, 4)
         assert route == miqmm.ROUTE_QMVX and tiles[0] == mt and tiles[1] in (1, 2, 4)
