@@ -162,6 +162,15 @@ def qmm_f64(x, w, s, b, K, group_size, bits, x_dtype=BF16, sb_dtype=BF16) -> np.
     return half_to_f32(x, x_dtype).astype(np.float64) @ wd.T
 
 
+def qmm_bf16w_f64(x, w, s, b, K, group_size, bits, x_dtype=BF16, sb_dtype=BF16) -> np.ndarray:
+    """The large-M route's arithmetic (MLX's qmm, reached from the reference's
+    prefill, src/engine/mlx_native.rs:1918-1922,2094-2102): W dequantized with
+    the fp32 fma, rounded to bf16 (the activation type of the dequantized
+    tiles), then multiplied exactly (float64) by x."""
+    wb = bf16_to_f32(f32_to_bf16(dequantize(w, s, b, K, group_size, bits, sb_dtype)))
+    return half_to_f32(x, x_dtype).astype(np.float64) @ wb.astype(np.float64).T
+
+
 def embedding(ids, w, s, b, K, group_size, bits, sb_dtype=BF16, out_dtype=BF16) -> np.ndarray:
     """out[..., k] = fma(s, q, b) of row ids[...] in fp32, rounded to out_dtype
     (bit patterns for bf16/fp16, float32 values for F32); an id outside

@@ -386,3 +386,35 @@ def test_embedding_out_of_range_and_rounding():
     assert f32.shape == (2, 2, K) and not f32[0, 1].any() and not f32[1, 0].any()
     h = O.embedding(ids, w, s, b, K, g, bits, out_dtype=O.BF16)
     np.testing.assert_array_equal(h, O.f32_to_bf16(f32))
+
+
+# ------------------------------------------------------------------ large-M route (bf16 weight tiles)
+def test_qmm_bf16w_equals_exact_when_weights_fit_bf16():
+    """With power-of-two scales and biases that keep s*q + b within 8
+    significant bits, the bf16 rounding of W changes nothing: the bf16-tile
+    product equals the exact one"""
+    rng = np.random.default_rng(5)
+    M, N, K, g, bits = 3, 16, 128, 32, 4
+    q = rng.integers(0, 16, size=(N, K)).astype(np.uint32)
+    w = O.pack(q, bits)
+    G = K // g
+    s = O.f32_to_bf16((2.0 ** rng.integers(-6, 3, size=(N, G))).astype(np.float32))
+    b = O.f32_to_bf16((rng.integers(-100, 100, size=(N, G)) * O.bf16_to_f32(s)).astype(np.float32))
+    x, _, _, _ = O.synth_problem(M, N, K, g, bits, seed=5, stream=2)
+    np.testing.assert_array_equal(O.qmm_bf16w_f64(x, w, s, b, K, g, bits), O.qmm_f64(x, w, s, b, K, g, bits))
+
+
+def test_qmm_bf16w_rounding_matches_torch():
+    """the weight tile rounding is round-to-nearest-even, checked against
+    torch's independent float32 -> bfloat16 conversion; a truncating
+    conversion (a plausible mistake) is rejected by the same comparison"""
+    import torch
+
+    M, N, K, g, bits = 2, 64, 256, 64, 4
+    x, w, s, b = O.synth_problem(M, N, K, g, bits, seed=6, stream=3)
+    wd = O.dequantize(w, s, b, K, g, bits)
+    wt = torch.from_numpy(wd).to(torch.bfloat16).to(torch.float64).numpy()
+    want = O.bf16_to_f32(x).astype(np.float64) @ wt.T
+    np.testing.assert_array_equal(O.qmm_bf16w_f64(x, w, s, b, K, g, bits), want)
+    trunc = (wd.view(np.uint32) & 0xFFFF0000).view(np.float32).astype(np.float64)
+    assert not np.array_equal(O.bf16_to_f32(x).astype(np.float64) @ trunc.T, want)
