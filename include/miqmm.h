@@ -52,8 +52,9 @@ typedef enum { MIQMM_DT_BF16 = 0, MIQMM_DT_F16 = 1, MIQMM_DT_F32 = 2 } miqmm_dty
  * with bf16-dequantized W tiles; QMV_DOT: small-M GEMV on v_dot2 (no MFMA);
  * QMVX: small-M GEMV on MFMA with x staged in LDS (M <= 4 per pass, needs
  * K/group_size even and min(M,4)*K <= 32768); QMVS: one-row GEMV on v_dot2
- * with K cut into 1 KiB slices of codes, one wave per slice (M == 1, needs
- * K*bits/8 <= 15 KiB, K/group_size even, scales and biases 4-byte aligned). */
+ * with K cut into 1 KiB slices of codes, one wave per slice, or two rows per
+ * wave on rows of at most 32 chunks (M == 1, needs K*bits/8 <= 15 KiB,
+ * K/group_size even, scales and biases 4-byte aligned). */
 typedef enum {
     MIQMM_ROUTE_AUTO = 0,
     MIQMM_ROUTE_QMV = 1,
@@ -70,8 +71,9 @@ typedef enum {
  * QuantizedLinear::forward).  transpose must be 1; bits in {4, 8};
  * group_size in {32, 64, 128}; K % group_size == 0; x and w 16-byte aligned.
  * M == 0 is a no-op.  Route (HBM-bound GEMVs for M <= 16): M == 1 -> qmvs
- * for K >= 2048 (with K*bits/8 <= 15 KiB, K/group_size even and 4-byte
- * aligned scales and biases), else qmv_dot, or qmvx for
+ * for K >= 2048 or rows of at most 32 16-byte chunks (K <= 1024 at 4 bits,
+ * 512 at 8; two rows per wave slice), with K*bits/8 <= 15 KiB, K/group_size
+ * even and 4-byte aligned scales and biases; else qmv_dot, or qmvx for
  * N >= 65536 with K <= 2048; 2 <= M <= 4 -> qmvx where supported, else
  * qmv_dot; M <= 16 -> qmv; else qmm (MFMA-bound tiled matmul).
  */
@@ -96,15 +98,25 @@ typedef struct miqmm_problem {
 
 /*
  * Several independent projections that share M, K, group_size, bits and
- * dtypes, as one v_dot2 GEMV launch per four problems when M <= 2 and every
- * N < 65536 (decode projections), else one call per problem on its own route.  This has no single counterpart
- * in the reference: it replaces the reference's separate quantized projections
- * that read the same activation -- q/k/v (src/engine/mlx_lm/models/llama.rs:
- * 195-197) and gate/up (:293-294) -- whose decode-step launches are otherwise
- * latency-bound.  In the grouped case each problem's result equals, bit for
- * bit, miqmm_quantized_matmul_ex with MIQMM_ROUTE_QMV_DOT on it alone (plus
- * the bias as miqmm_quantized_linear adds it); otherwise it equals
- * miqmm_quantized_matmul (or miqmm_quantized_linear) on it alone.
+ * dtypes.  When M <= 2 and every N < 65536 (decode projections) they run as
+ * one launch per four problems:
+ *  - M == 1, up to four problems sharing x whose codes, scales and biases lie
+ *    one after another in memory (a loader that fuses q/k/v or gate/up), on
+ *    rows the K-sliced GEMV takes (K >= 2048, or at most 32 16-byte chunks
+ *    per row) with 4-byte aligned scales: one K-sliced GEMV over all their
+ *    rows, each row stored to its problem's output; every result equals,
+ *    bit for bit, the matching rows of miqmm_quantized_matmul_ex with
+ *    MIQMM_ROUTE_QMVS on the fused matrix (plus the bias as
+ *    miqmm_quantized_linear adds it);
+ *  - otherwise one v_dot2 GEMV launch per four problems, each result equal,
+ *    bit for bit, to miqmm_quantized_matmul_ex with MIQMM_ROUTE_QMV_DOT on it
+ *    alone (plus the bias).
+ * Else one call per problem on its own route, each equal to
+ * miqmm_quantized_matmul (or miqmm_quantized_linear) on it alone.  This has
+ * no single counterpart in the reference: it replaces the reference's
+ * separate quantized projections that read the same activation -- q/k/v
+ * (src/engine/mlx_lm/models/llama.rs:195-197) and gate/up (:293-294) --
+ * whose decode-step launches are otherwise latency-bound.
  */
 int miqmm_quantized_matmul_grouped(const miqmm_problem* problems, int count, int64_t M, int64_t K,
                                    int group_size, int bits, int x_dtype, int sb_dtype, int y_dtype,
