@@ -1,7 +1,8 @@
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-headline]
-    python bench.py --profile-target {step,qkv,o,gateup,down,lm_head,qmv,qmv_down,config0,qmm,read33,read77,copy}
+    python bench.py --profile-target {step,qkv,o,gateup,down,lm_head,qmv,qmv_down,config0,qmv_m8,qmv_m8_down,
+                                      qmv_m16,qmv_m16_down,qmm,read33,read77,copy}
 
 Workload (one "step", the line's `value`): the linear layers of one
 Qwen2.5-0.5B decode step at M=1, 4-bit group-64 affine weights with bf16
@@ -467,10 +468,13 @@ def profile_section(miqmm, torch, target):
         sec, nb = step_type_line(miqmm, torch, Ns, K)
         return {"section": target, "shapes": [(N, K) for N in Ns], "replays": REPS,
                 **line(sec, nb)}
-    if target in ("qmv", "qmv_down", "config0"):
-        N, K = {"qmv": (14336, 4096), "qmv_down": (4096, 14336), "config0": (4864, 896)}[target]
-        sec, nb = gemv_line(miqmm, torch, 1, N, K)
-        return {"section": target, "shape": f"M=1 N={N} K={K}", "replays": REPS, **line(sec, nb)}
+    gemvs = {"qmv": (1, 14336, 4096), "qmv_down": (1, 4096, 14336), "config0": (1, 4864, 896),
+             "qmv_m8": (8, 14336, 4096), "qmv_m8_down": (8, 4096, 14336),
+             "qmv_m16": (16, 14336, 4096), "qmv_m16_down": (16, 4096, 14336)}
+    if target in gemvs:
+        M, N, K = gemvs[target]
+        sec, nb = gemv_line(miqmm, torch, M, N, K)
+        return {"section": target, "shape": f"M={M} N={N} K={K}", "replays": REPS, **line(sec, nb)}
     if target in ("read33", "read77"):
         sec, nb = read_ceiling(miqmm, torch, 33067008 if target == "read33" else 76881408)
         return {"section": target, "replays": REPS, **line(sec, nb)}
@@ -504,8 +508,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-headline", action="store_true")
     ap.add_argument("--profile-target", default=None,
-                    choices=["step", "qkv", "o", "gateup", "down", "lm_head", "qmv", "qmv_down", "config0", "qmm",
-                             "read33", "read77", "copy"],
+                    choices=["step", "qkv", "o", "gateup", "down", "lm_head", "qmv", "qmv_down", "config0",
+                             "qmv_m8", "qmv_m8_down", "qmv_m16", "qmv_m16_down", "qmm", "read33", "read77", "copy"],
                     help="run only this measured section and print its figures (for rocprofv3 summaries)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

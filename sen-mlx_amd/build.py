@@ -36,9 +36,15 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
+# per-file flags: the small-M MFMA GEMV keeps its few accumulators in VGPRs,
+# where the dequant's fused multiply-adds read them directly (in AGPRs every
+# read is a copy)
+FILE_FLAGS = {"qmv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *FLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *FLAGS, *FILE_FLAGS.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:

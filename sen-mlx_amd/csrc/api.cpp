@@ -194,7 +194,9 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
             part.x = static_cast<const uint16_t*>(x) + m0 * K;
             const int ysz = y_dtype == MIQMM_DT_F32 ? 4 : 2;
             part.y = static_cast<char*>(y) + m0 * N * ysz;
-            st = route == MIQMM_ROUTE_QMV    ? check_launch(miqmm::launch_qmv_mfma(part), "qmv launch")
+            st = route == MIQMM_ROUTE_QMV    ? check_launch(miqmm::launch_qmv_mfma_split(part, workspace,
+                                                                                         workspace_bytes),
+                                                            "qmv launch")
                  : route == MIQMM_ROUTE_QMVX ? check_launch(miqmm::launch_qmvx(part), "qmvx launch")
                                              : check_launch(miqmm::launch_qmv(part), "qmv_dot launch");
             if (st != MIQMM_OK) return st;
@@ -206,14 +208,15 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
 
 // bytes of k-split partials the auto route takes for a shape (0: none)
 int64_t split_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size, int bits) {
-    if (auto_route(M, N, K, group_size, bits) != MIQMM_ROUTE_QMM) return 0;
+    const int route = auto_route(M, N, K, group_size, bits);
+    if (route != MIQMM_ROUTE_QMM && route != MIQMM_ROUTE_QMV) return 0;
     miqmm::QmmArgs a{};
     a.M = M;
     a.N = N;
     a.K = K;
     a.group_size = group_size;
     a.bits = bits;
-    return miqmm::qmm_workspace_bytes(a);
+    return route == MIQMM_ROUTE_QMM ? miqmm::qmm_workspace_bytes(a) : miqmm::qmv_split_bytes(a);
 }
 
 

@@ -60,6 +60,13 @@ bool qmv_ksplit(int64_t M, int64_t N, int64_t K, int bits);
 hipError_t launch_qmv_gather(const QmmArgs& a, const int32_t* idx, int64_t T, int top_k, int x_per_expert,
                              int64_t experts, int64_t x_stride, int64_t y_stride);
 hipError_t launch_qmv_mfma(const QmmArgs& a);  // group-diagonal MFMA GEMV
+// the same with its K split over blocks when `workspace_bytes` holds the
+// partials (qmv_split_bytes; less, nullptr or unaligned scales: unsplit)
+hipError_t launch_qmv_mfma_split(const QmmArgs& a, void* workspace, int64_t workspace_bytes);
+// workspace bytes of the MFMA GEMV's K split for this shape (0: unsplit)
+int64_t qmv_split_bytes(const QmmArgs& a);
+// y = sum of ks fp32 partial planes [ks][M][N] in order, in y's dtype, + bias
+hipError_t launch_split_reduce(const float* part, int ks, const QmmArgs& a);
 // workspace: fp32 partials of a k split (the plan splits only where
 // workspace_bytes holds them; nullptr / 0: never split)
 hipError_t launch_qmm(const QmmArgs& a, void* workspace = nullptr, int64_t workspace_bytes = 0);

@@ -507,46 +507,44 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
 
 // y = sum over z of part[z] (z = 0 .. ks-1 in order, the same bits for any
 // grid), rounded to y's dtype (+ bias as a separate rounding): one thread per
-// run of 8 outputs of a row
+// run of 4 outputs of a row, four planes' loads in flight at a time (a few
+// rows of x give few threads, each with ks planes to add)
 __global__ __launch_bounds__(256) void qmm_split_reduce_kernel(const float* __restrict__ part, int ks, int M, int N,
                                                                void* __restrict__ y, const void* __restrict__ bias,
                                                                int y_dtype) {
-    const int runs = (N + 7) / 8;
+    const int runs = (N + 3) / 4;
     const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (q >= (int64_t)M * runs) return;
-    const int gr = (int)(q / runs), gc = (int)(q % runs) * 8;
+    const int gr = (int)(q / runs), gc = (int)(q % runs) * 4;
     const int64_t o = (int64_t)gr * N + gc;
     const int64_t plane = (int64_t)M * N;
-    const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
-    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int z = 0; z < ks; ++z) {
+    const bool vec = (N & 3) == 0;
+    auto ld = [&](int z) {
         const float* p = part + z * plane + o;
-        if (vec) {
-            const f32x4_t a = *reinterpret_cast<const f32x4_t*>(p), b = *reinterpret_cast<const f32x4_t*>(p + 4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[e] += a[e];
-                v[4 + e] += b[e];
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (gc + e < N) v[e] += p[e];
-        }
-    }
-    if (vec && y_dtype != DT_F32) {
-        u32x4_t h;
+        if (vec) return *reinterpret_cast<const f32x4_t*>(p);
+        f32x4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            h[e] = (uint32_t)out_half_bits(y_dtype, v[2 * e], bias, gc + 2 * e) |
-                   ((uint32_t)out_half_bits(y_dtype, v[2 * e + 1], bias, gc + 2 * e + 1) << 16);
-        *reinterpret_cast<u32x4_t*>((uint16_t*)y + o) = h;
-    } else {
+            if (gc + e < N) a[e] = p[e];
+        return a;
+    };
+    f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+    int z = 0;
+    for (; z + 4 <= ks; z += 4) {
+        const f32x4_t a = ld(z), b = ld(z + 1), c = ld(z + 2), d = ld(z + 3);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            if (gc + e < N) store_out(y, o + e, y_dtype, v[e], bias, gc + e);
+        for (int e = 0; e < 4; ++e) v[e] = (((v[e] + a[e]) + b[e]) + c[e]) + d[e];
     }
+    for (; z < ks; ++z) {
+        const f32x4_t a = ld(z);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += a[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (gc + e < N) store_out(y, o + e, y_dtype, v[e], bias, gc + e);
 }
+
 
 template <int BITS, int SBT, int BN, bool GATHER>
 hipError_t launch_t(const QmmArgs& a, const QmmGather& gq, int64_t m_tiles, const QmmSplit& sp) {
@@ -644,6 +642,19 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int max_ks) {
     return best;
 }
 
+}  // namespace
+
+// y = the sum of ks fp32 partial planes [ks][M][N] (in order), rounded to y's
+// dtype, plus the bias
+hipError_t launch_split_reduce(const float* part, int ks, const QmmArgs& a) {
+    const int64_t threads = a.M * ((a.N + 3) / 4);
+    hipLaunchKernelGGL(qmm_split_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a.stream,
+                       part, ks, (int)a.M, (int)a.N, a.y, a.bias, a.y_dtype);
+    return hipGetLastError();
+}
+
+namespace {
+
 constexpr int kMaxSplit = 4;
 
 // the plan with k ranges only where `workspace_bytes` holds their partials
@@ -662,10 +673,7 @@ hipError_t launch_bn(const QmmArgs& a, void* workspace, int64_t workspace_bytes)
     hipError_t e = pl.bn == 256 ? launch_t<BITS, SBT, 256, false>(a, none, mt, sp)
                                 : launch_t<BITS, SBT, 128, false>(a, none, mt, sp);
     if (e != hipSuccess || pl.ks == 1) return e;
-    const int64_t threads = a.M * ((a.N + 7) / 8);
-    hipLaunchKernelGGL(qmm_split_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, a.stream,
-                       static_cast<const float*>(workspace), pl.ks, (int)a.M, (int)a.N, a.y, a.bias, a.y_dtype);
-    return hipGetLastError();
+    return launch_split_reduce(static_cast<const float*>(workspace), pl.ks, a);
 }
 
 template <int BITS, int SBT>

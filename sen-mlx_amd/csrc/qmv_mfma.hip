@@ -28,9 +28,29 @@
 //   This keeps the dequant exact (fp32, as the reference's fp32 fma) and
 //   needs ~1 VALU op per code.
 //
+// Group cycles: the per-group dequant is applied once per cycle of GS
+// groups.  A cycle of up to 8 k-blocks starts and ends at fixed k-blocks of
+// a pipeline iteration (two k-quads; a wave's range starts an iteration and a
+// cycle), so its first MFMAs take a zero accumulator and its last k-block
+// folds D into the totals with no clearing; longer cycles span whole
+// iterations.  The accumulators live in VGPRs (built with
+// -amdgpu-mfma-vgpr-form), where the fused multiply-adds read them directly.
+// Together: 26.5 -> 16.4 VALU instructions per MFMA (M = 16, 4-bit g64).
+//
 // Work split: a block owns T tiles of 16 output rows n and all of K; its WPB
 // waves split K into contiguous k-quad ranges (a k-quad is 4 k-blocks = 128
 // codes) and combine their partial sums through LDS at the end.
+//
+// K split (SPLIT, with a caller workspace): blocks of 8 waves own a tile each
+// over one of S k ranges; the block stages its x range in LDS once, as the
+// A rows already masked to their group slot and permuted for the code unpack,
+// each wave streams its tile's codes four k-quads ahead, and writes fp32
+// partials that the split-reduce kernel adds in range order.  What bounds the
+// kernel is the bytes a CU loads: each CU's vector-memory path delivers
+// about 30 GB/s whether a load hits L1, L2 or HBM (measured on MI355X: 16
+// rows of x re-read by every block, 4.6-9 TB/s in total; the same bytes read
+// by the four waves of a block from L1, the same time), so x re-read per
+// block of 16-64 rows costs as much as the codes at M = 16.
 //
 // Scales and biases: each wave copies those of its k range for the block's
 // rows into its own LDS area when it starts (direct-to-LDS dword loads, ahead
@@ -75,12 +95,27 @@ __device__ __forceinline__ void transpose4x4(u32x4_t& v) {
     v[3] = d[1];
 }
 
-// group pairs per row that a wave stages: the whole group cycles (GS groups)
-// its k range (QS k-quads of 128 codes) touches, from an even group on; and
-// the pairs of one array (scales or biases) of a wave's LDS area: rows x
-// pairs, rounded up to whole 64-lane direct-to-LDS loads
+// log2 of the k-blocks (32 codes) of one group cycle (GS groups of 2^gs_shift
+// codes), and the cycle class a kernel is built for: 0-3 a cycle of 1-8
+// k-blocks, which starts and ends at fixed places of the two k-quads of a
+// pipeline iteration; 4 a longer cycle, a whole number of iterations
+__host__ __device__ constexpr int cycle_shift(int gs_shift, int gs) { return gs_shift - 5 + __builtin_ctz(gs); }
+__host__ __device__ constexpr int cycle_class(int cl_shift) { return cl_shift <= 3 ? cl_shift : 4; }
+// k-quads per wave: the K split over the block's waves, in whole iterations
+// (two k-quads) and whole group cycles, so every wave starts a cycle
+__host__ __device__ constexpr int wave_kquads(int K, int wpb, int cl_shift) {
+    const int span = cl_shift <= 3 ? 2 : 1 << (cl_shift - 2);
+    return ((((K >> 5) + 3) >> 2) + wpb - 1) / wpb + span - 1 & ~(span - 1);
+}
+// SPLIT: bytes per A row of the block's x in LDS (qs k-quads of 128 codes;
+// 16 bytes of padding put the 16 rows of an operand read in different banks)
+__host__ __device__ constexpr int split_x_stride(int qs) { return qs * 256 + 16; }
+// group pairs per row that a wave stages (those of its k range: a whole
+// number of pairs, its k range spans an even number of k-quads), and the
+// pairs of one array (scales or biases) of a wave's LDS area: rows x pairs,
+// rounded up to whole 64-lane direct-to-LDS loads
 __host__ __device__ constexpr int sb_pairs(int K, int gs_shift, int wpb, int gs) {
-    return (((((K >> 5) + 3) >> 2) + wpb - 1) / wpb * (128 >> gs_shift) + 2 * gs + 1) / 2 + 1;
+    return (wave_kquads(K, wpb, cycle_shift(gs_shift, gs)) << (7 - gs_shift)) >> 1;
 }
 __host__ __device__ constexpr int sb_area_pairs(int T, int npr) { return (16 * T * npr + 63) / 64 * 64; }
 
@@ -109,14 +144,19 @@ __device__ __forceinline__ int sload(const int32_t* p) {  // wave-uniform scalar
     return __builtin_amdgcn_readfirstlane(*(const __attribute__((address_space(4))) int32_t*)p);
 }
 
-template <int BITS, int SBT, int MT, int T, int WPB, bool GATHER, bool SBL>
+// CLS: the cycle class (cycle_class) of the launch's group size and MT.
+// SPLIT: K is cut into ksplit ranges (blockIdx.y), the waves of a block own
+// different tiles over one range, and each wave writes its fp32 partial sums
+// to y = partials [ksplit][M][N] (added in range order by the split-reduce
+// kernel); otherwise a block's waves split K over its tiles.
+template <int BITS, int SBT, int MT, int T, int WPB, bool GATHER, bool SBL, int CLS, bool SPLIT>
 __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __restrict__ x,
                                                             const uint32_t* __restrict__ w,
                                                             const uint16_t* __restrict__ sc,
                                                             const uint16_t* __restrict__ bi,
                                                             void* __restrict__ y,
                                                             const void* __restrict__ bias, int M, int N,
-                                                            int K, int gs_shift, int y_dtype,
+                                                            int K, int gs_shift, int y_dtype, int ksplit,
                                                             const MfmaGather g = MfmaGather{}) {
     constexpr int GS = 16 / MT;                 // group slots per m
     constexpr int NMT = MT >= 4 ? MT / 4 : 1;   // distinct m per lane
@@ -124,27 +164,36 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
     using St = QStage<BITS, T>;
     // vector-memory loads of one stage: the codes (4-bit: one per tile;
     // 8-bit: two 8-byte loads per tile and register) and four x loads
-    constexpr int kStageLoads = (BITS == 4 ? T : 4 * T) + 4;
+    // (SPLIT: x comes from LDS, no x loads)
+    constexpr int kStageLoads = (BITS == 4 ? T : 4 * T) + (SPLIT ? 0 : 4);
     // stages in flight (measured on MI355X, M = 16 on 4096 -> 14336: 26.3,
     // 27.0 and 28.1 us with 2, 3 and 4)
-    constexpr int DEPTH = 2;
-    static_assert(DEPTH * kStageLoads < 64, "vmcnt range");
+#ifndef QMV_MFMA_DEPTH
+#define QMV_MFMA_DEPTH 2
+#endif
+    constexpr int kMaxDepth = (63 / kStageLoads) & ~1;  // the loads a vmcnt wait can count
+    // SPLIT stages hold only codes: four k-quads in flight (measured on
+    // MI355X, M = 16: 4096 -> 14336 15.5 / 16.2 / 18.2 us with 4 / 8 / 16)
+    constexpr int kDepth = SPLIT ? 4 : QMV_MFMA_DEPTH;
+    constexpr int DEPTH = kDepth < kMaxDepth ? kDepth : kMaxDepth;
+    static_assert(DEPTH >= 2 && DEPTH * kStageLoads < 64, "vmcnt range");
 
-    extern __shared__ float red[];  // [WPB][T][64 lanes][NMT], then the waves' scale / bias areas
+    // [WPB][T][64 lanes][NMT] (not with SPLIT), then the waves' scale / bias areas
+    extern __shared__ float red[];
 
     const int lane = threadIdx.x & 63;
     const int nl = lane & 15, q = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n0 = blockIdx.x * 16 * T;
+    const int n0 = (SPLIT ? blockIdx.x * WPB + wv : blockIdx.x) * 16 * T;
     const int KB = K >> 5;            // k-blocks of 32 codes
     const int KQ = (KB + 3) >> 2;     // k-quads
-    const int QS = (KQ + WPB - 1) / WPB;
-    const int u0 = wv * QS;
+    const int cl_shift = CLS < 4 ? CLS : cycle_shift(gs_shift, GS);  // log2(k-blocks per GS-group cycle)
+    const int QS = wave_kquads(K, SPLIT ? ksplit : WPB, cl_shift);
+    const int u0 = (SPLIT ? (int)blockIdx.y : wv) * QS;
     const int u1 = min(u0 + QS, KQ);
     const int G = K >> gs_shift;
-    const int cl_shift = gs_shift - 5 + __builtin_ctz(GS);  // log2(k-blocks per GS-group cycle)
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
-    int rows_here = min(16 * T, N - n0);
+    int rows_here = max(0, min(16 * T, N - n0));
     size_t erow0 = 0;  // GATHER: first W row of the expert
     int p0 = 0;        // GATHER: first position of the tile in the selection list
     if constexpr (GATHER) {
@@ -204,26 +253,35 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
                 }
             }
         }
+        if constexpr (!SPLIT) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int kb = 4 * u + i;
-            const int gidx = kb >> (gs_shift - 5);
-            const bool live = kb < kbe && xrow != kOOB && (gidx % GS) == slot_a;
-            st.xa[i] = bload16(xr, live ? xrow + (uint32_t)(kb * 32 + 8 * q) * 2 : kOOB);
+            for (int i = 0; i < 4; ++i) {
+                const int kb = 4 * u + i;
+                const int gidx = kb >> (gs_shift - 5);
+                const bool live = kb < kbe && xrow != kOOB && (gidx % GS) == slot_a;
+                st.xa[i] = bload16(xr, live ? xrow + (uint32_t)(kb * 32 + 8 * q) * 2 : kOOB);
+            }
         }
     };
 
-    // apply the dequant of one group cycle c (groups c*GS .. c*GS+GS-1) and clear D
+    // apply the dequant of one group cycle c (groups c*GS .. c*GS+GS-1): the
+    // next cycle's first MFMAs start from zero (CLS < 4) or D is cleared at
+    // the next cycle's start (CLS 4).
     // This lane's four D rows r = 4q + j hold groups c*GS + r % GS: with
     // GS < 4 only GS of them differ (r % GS = j % GS), so each distinct
     // scale / bias is loaded once (M = 16: one pair per row instead of four)
     constexpr int NG = GS < 4 ? GS : 4;
     // this wave's LDS area (SBL): scales then biases, [16T rows][2 npr]
-    // halves of groups g0 .. g0 + 2 npr - 1, from the first group of its
-    // first cycle rounded down to even, zero past G
-    const int npr = sb_pairs(K, gs_shift, WPB, GS), area = sb_area_pairs(T, npr);
-    const int g0 = ((u0 << (7 - gs_shift)) / GS * GS) & ~1;
-    uint16_t* const sl = reinterpret_cast<uint16_t*>(red + WPB * T * 64 * NMT) + wv * 4 * area;
+    // halves of groups g0 .. g0 + 2 npr - 1, the groups of its k range (its
+    // first group starts a cycle and is even), zero past G
+    const int npr = sb_pairs(K, gs_shift, SPLIT ? ksplit : WPB, GS), area = sb_area_pairs(T, npr);
+    const int g0 = u0 << (7 - gs_shift);
+    // SPLIT: the block's A rows (m, slot) of x over its k range, then the scale areas
+    char* const xs = reinterpret_cast<char*>(red);
+    const int xstride = split_x_stride(QS);
+    const int xa_lane = nl * xstride + q * 16;  // this lane's A operand in a k-block's 64-byte run
+    uint16_t* const sl =
+        reinterpret_cast<uint16_t*>(red + (SPLIT ? 4 * xstride : WPB * T * 64 * NMT)) + wv * 4 * area;
     uint16_t* const bl = sl + 2 * area;
     auto rescale = [&](int c) {
 #pragma unroll
@@ -253,13 +311,21 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
                 tot[t][mi] = fmaf(s, D[t][j], tot[t][mi]);
                 tot[t][mi] = fmaf(b, DX[j], tot[t][mi]);
             }
-            D[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         }
+    };
+    auto clear = [&] {
+#pragma unroll
+        for (int t = 0; t < T; ++t) D[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         DX = f32x4_t{0.f, 0.f, 0.f, 0.f};
     };
 
     const u32x4_t ones = {kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
-    auto compute = [&](int u, St& st) {
+    // k-quad u, the POS-th (0 or 1) of its pipeline iteration.  With CLS < 4
+    // a cycle of 2^CLS k-blocks starts and ends at fixed k-blocks of the
+    // iteration: its first MFMAs take a zero accumulator and its last folds
+    // it into the totals, with no clearing of D.
+    auto compute = [&](int u, St& st, auto pos) {
+        constexpr int POS = decltype(pos)::value;
         if constexpr (BITS == 4) {
 #pragma unroll
             for (int t = 0; t < T; ++t) transpose4x4(st.code[t]);
@@ -267,8 +333,15 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int kb = 4 * u + i;
+            constexpr int CB = 1 << (CLS < 4 ? CLS : 0);
+            const int p = 4 * POS + i;  // k-block of the iteration
+            const bool restart = CLS < 4 && (p & (CB - 1)) == 0;
+            const bool end = CLS < 4 && (p & (CB - 1)) == CB - 1;
             u32x4_t a;
-            if constexpr (BITS == 4) {
+            if constexpr (SPLIT) {
+                // A row nl of this k-block, staged (masked, permuted) in LDS
+                a = *reinterpret_cast<const u32x4_t*>(xs + xa_lane + (kb - 4 * u0) * 64);
+            } else if constexpr (BITS == 4) {
                 uint32_t xw[4] = {st.xa[i][0], st.xa[i][1], st.xa[i][2], st.xa[i][3]};
                 uint32_t X[4];
                 perm_x_for4(xw, X);
@@ -277,30 +350,60 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
                 a = st.xa[i];
             }
             const bf16x8_t A = as_bf16x8(a);
+            const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                uint32_t p[4];
+                uint32_t pw[4];
                 if constexpr (BITS == 4) {
-                    unpack4_magic(st.code[t][i], p, kMask, kMagic);
+                    unpack4_magic(st.code[t][i], pw, kMask, kMagic);
                 } else {
                     // quad q of k-block 4u+i: words 2*(i&1), 2*(i&1)+1 of register 2t + i/2
                     const u32x4_t& c = st.code[2 * t + (i >> 1)];
-                    unpack8_pairs(c[2 * (i & 1)], &p[0]);
-                    unpack8_pairs(c[2 * (i & 1) + 1], &p[2]);
+                    unpack8_pairs(c[2 * (i & 1)], &pw[0]);
+                    unpack8_pairs(c[2 * (i & 1) + 1], &pw[2]);
                 }
-                D[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(u32x4_t{p[0], p[1], p[2], p[3]}), D[t], 0, 0, 0);
+                D[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(u32x4_t{pw[0], pw[1], pw[2], pw[3]}),
+                                                               restart ? zero : D[t], 0, 0, 0);
             }
-            DX = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(ones), DX, 0, 0, 0);
-            // end of a group cycle (or of K): fold the cycle into the totals
-            if (kb < KB && (((kb + 1) >> cl_shift) != (kb >> cl_shift) || kb + 1 == KB)) rescale(kb >> cl_shift);
+            DX = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, as_bf16x8(ones), restart ? zero : DX, 0, 0, 0);
+            if (end) rescale(kb >> cl_shift);
         }
     };
 
-    // pipeline over k-quads, DEPTH stages in flight.  Each stage is
-    // refilled right after it is computed, unconditionally: a conditional
-    // issue makes the compiler's wait before each compute count from the path
-    // without the loads, i.e. wait for the stage just issued.
-    if (u0 < u1) {
+    // pipeline over iterations of two k-quads, one stage each in flight.
+    // Each stage is refilled right after it is computed, unconditionally: a
+    // conditional issue makes the compiler's wait before each compute count
+    // from the path without the loads, i.e. wait for the stage just issued.
+    if (u0 < u1) {  // (SPLIT: true for every block)
+        // SPLIT: the block's x over its k range as the MFMA's A rows: row r =
+        // (m, slot) holds x[m] where the group is slot mod GS (zero elsewhere
+        // and past M or K), 4-bit: in the code unpack's pair order; each 16
+        // bytes loaded once per block, up to XU per thread ahead of the codes
+        constexpr int XU = 8;
+        const int units = SPLIT ? 16 * QS * 16 : 0;  // rows x 16-byte units of the range
+        u32x4_t xv[XU];
+        auto x_unit = [&](int e, bool load) {
+            const int r = e / (QS * 16), c8 = e - r * (QS * 16);
+            const int m = r / GS, slot = r % GS;
+            const int k = u0 * 128 + c8 * 8;
+            const bool live = e < units && m < M && k < K && ((k >> gs_shift) & (GS - 1)) == slot;
+            return load ? bload16(xr, live ? (uint32_t)(m * K + k) * 2 : kOOB)
+                        : u32x4_t{(uint32_t)(r * xstride + c8 * 16), (uint32_t)(e < units), 0u, 0u};
+        };
+        auto x_store = [&](int e, u32x4_t v) {
+            const u32x4_t at = x_unit(e, false);
+            if (!at[1]) return;
+            if constexpr (BITS == 4) {
+                uint32_t xw[4] = {v[0], v[1], v[2], v[3]}, X[4];
+                perm_x_for4(xw, X);
+                v = u32x4_t{X[0], X[1], X[2], X[3]};
+            }
+            *reinterpret_cast<u32x4_t*>(xs + at[0]) = v;
+        };
+        if constexpr (SPLIT) {
+#pragma unroll
+            for (int j = 0; j < XU; ++j) xv[j] = x_unit(threadIdx.x + j * WPB * 64, true);
+        }
         if constexpr (SBL) {  // stage the scales and biases, ahead of the stages' loads
             const int npairs = 16 * T * npr;
             for (int d = 0; d * 64 < npairs; ++d) {
@@ -314,26 +417,67 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
         St S[DEPTH];
 #pragma unroll
         for (int i = 0; i < DEPTH; ++i) issue(u0 + i, S[i]);
+        if constexpr (SPLIT) {
+#pragma unroll
+            for (int j = 0; j < XU; ++j) x_store(threadIdx.x + j * WPB * 64, xv[j]);
+            for (int e = threadIdx.x + XU * WPB * 64; e < units; e += WPB * 64) x_store(e, x_unit(e, true));
+            __syncthreads();
+            if (rows_here == 0) return;  // a wave past N (after the block's barrier)
+        }
         // the staged scales land before any cycle reads them (the compiler
         // does not see that dependency): issued after them and still allowed
         // in flight are the stages' loads
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_waitcnt(waitcnt_vm(DEPTH * kStageLoads));
         asm volatile("" ::: "memory");
+        // CLS 4: a cycle of 2^cl_shift k-blocks spans whole iterations
+        const int cb_mask = (1 << cl_shift) - 1;
+        // the k-quads uu (and uu + 1 when two) of one iteration
+        auto iteration = [&](int uu, St& s0, St& s1, bool two) {
+            if constexpr (CLS == 4)
+                if (((4 * uu) & cb_mask) == 0) clear();
+            compute(uu, s0, std::integral_constant<int, 0>{});
+            if (two) compute(uu + 1, s1, std::integral_constant<int, 1>{});
+            // CLS 4: the cycle ends with the iteration, or the range does;
+            // CLS 3: a single k-quad ends its cycle part-filled
+            if constexpr (CLS == 4) {
+                if (((4 * (uu + 2)) & cb_mask) == 0 || uu + 2 >= u1) rescale((4 * uu) >> cl_shift);
+            } else if constexpr (CLS == 3) {
+                if (!two) rescale((4 * uu) >> cl_shift);
+            }
+        };
         int u = u0;
         for (; u + DEPTH <= u1; u += DEPTH) {
 #pragma unroll
-            for (int i = 0; i < DEPTH; ++i) {
-                compute(u + i, S[i]);
+            for (int i = 0; i < DEPTH; i += 2) {
+                if constexpr (CLS == 4)
+                    if (((4 * (u + i)) & cb_mask) == 0) clear();
+                compute(u + i, S[i], std::integral_constant<int, 0>{});
                 issue(u + i + DEPTH, S[i]);
+                compute(u + i + 1, S[i + 1], std::integral_constant<int, 1>{});
+                issue(u + i + 1 + DEPTH, S[i + 1]);
+                if constexpr (CLS == 4)
+                    if (((4 * (u + i + 2)) & cb_mask) == 0 || u + i + 2 == u1) rescale((4 * (u + i)) >> cl_shift);
             }
         }
 #pragma unroll
-        for (int i = 0; i + 1 < DEPTH; ++i)
-            if (u + i < u1) compute(u + i, S[i]);
-        // a slice that ends mid-cycle has partial sums left in D
-        const int last = min(4 * u1, KB) - 1;
-        if (((last + 1) >> cl_shift) == (last >> cl_shift) && last + 1 != KB) rescale(last >> cl_shift);
+        for (int i = 0; i < DEPTH; i += 2)  // the k-quads left, fewer than DEPTH
+            if (u + i < u1) iteration(u + i, S[i], S[i + 1], u + i + 1 < u1);
+    }
+
+    if constexpr (SPLIT) {
+        // this wave's partial sums of its range: lane (nl, q) holds m = q NMT + i of row n0 + 16 t + nl
+        float* const part = static_cast<float*>(y) + (size_t)blockIdx.y * M * N;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int n = n0 + 16 * t + nl;
+#pragma unroll
+            for (int i = 0; i < NMT; ++i) {
+                const int m = q * NMT + i;
+                if (m < M && n < N) part[(size_t)m * N + n] = tot[t][i];
+            }
+        }
+        return;
     }
 
     // combine the waves' partial sums and store
@@ -373,7 +517,7 @@ size_t mfma_lds(const QmmArgs& a, int T, int wpb, int mt, int nmt, int* sbl) {
     const int npr = sb_pairs((int)a.K, __builtin_ctz((unsigned)a.group_size), wpb, 16 / mt);
     const size_t stage = (size_t)wpb * 2 * sb_area_pairs(T, npr) * 4;
     const bool al = ((reinterpret_cast<uintptr_t>(a.scales) | reinterpret_cast<uintptr_t>(a.biases)) & 3) == 0;
-    *sbl = (a.K / a.group_size) % 2 == 0 && al && red + stage <= 160 * 1024 ? 1 : 0;
+    *sbl = *sbl && (a.K / a.group_size) % 2 == 0 && al && red + stage <= 160 * 1024 ? 1 : 0;
     return red + (*sbl ? stage : 0);
 }
 // dynamic LDS above the default 64 KiB needs the kernel's attribute raised,
@@ -391,48 +535,68 @@ hipError_t allow_lds(size_t lds) {
     return e;
 }
 
-template <int BITS, int SBT, int MT, int T, int WPB, bool GATHER, bool SBL>
-hipError_t launch_k(const QmmArgs& a, dim3 grid, size_t lds, const MfmaGather& g) {
-    const hipError_t e = allow_lds<qmv_mfma_kernel<BITS, SBT, MT, T, WPB, GATHER, SBL>>(lds);
+template <int BITS, int SBT, int MT, int T, int WPB, bool GATHER, bool SBL, int CLS, bool SPLIT>
+hipError_t launch_kc(const QmmArgs& a, dim3 grid, size_t lds, const MfmaGather& g, float* part) {
+    constexpr auto kernel = qmv_mfma_kernel<BITS, SBT, MT, T, WPB, GATHER, SBL, CLS, SPLIT>;
+    const hipError_t e = allow_lds<kernel>(lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((qmv_mfma_kernel<BITS, SBT, MT, T, WPB, GATHER, SBL>), grid, dim3(WPB * 64), lds, a.stream,
-                       (const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y,
-                       GATHER ? nullptr : a.bias, GATHER ? MT : (int)a.M, (int)a.N, (int)a.K,
-                       __builtin_ctz((unsigned)a.group_size), a.y_dtype, g);
+    hipLaunchKernelGGL(kernel, grid, dim3(WPB * 64), lds, a.stream, (const uint16_t*)a.x, a.w,
+                       (const uint16_t*)a.scales, (const uint16_t*)a.biases, SPLIT ? (void*)part : a.y,
+                       GATHER || SPLIT ? nullptr : a.bias, GATHER ? MT : (int)a.M, (int)a.N, (int)a.K,
+                       __builtin_ctz((unsigned)a.group_size), a.y_dtype, (int)grid.y, g);
     return hipGetLastError();
+}
+
+// the kernel of the launch's cycle class: group sizes 32, 64 and 128 give
+// three consecutive classes from log2(16 / MT) on
+template <int BITS, int SBT, int MT, int T, int WPB, bool GATHER, bool SBL, bool SPLIT = false>
+hipError_t launch_k(const QmmArgs& a, dim3 grid, size_t lds, const MfmaGather& g, float* part = nullptr) {
+    constexpr int L = __builtin_ctz(16 / MT);
+    constexpr int C0 = cycle_class(L), C1 = cycle_class(L + 1), C2 = cycle_class(L + 2);
+    const int cls = cycle_class(cycle_shift(__builtin_ctz((unsigned)a.group_size), 16 / MT));
+    if (cls == C0) return launch_kc<BITS, SBT, MT, T, WPB, GATHER, SBL, C0, SPLIT>(a, grid, lds, g, part);
+    if (cls == C1) return launch_kc<BITS, SBT, MT, T, WPB, GATHER, SBL, C1, SPLIT>(a, grid, lds, g, part);
+    return launch_kc<BITS, SBT, MT, T, WPB, GATHER, SBL, C2, SPLIT>(a, grid, lds, g, part);
 }
 
 template <int BITS, int SBT, int MT, int T, int WPB>
 hipError_t launch_t(const QmmArgs& a) {
     constexpr int NMT = MT >= 4 ? MT / 4 : 1;
     const dim3 grid((unsigned)((a.N + 16 * T - 1) / (16 * T)));
-    int sbl = 0;
+    int sbl = 1;
     const size_t lds = mfma_lds(a, T, WPB, MT, NMT, &sbl);
-    return sbl ? launch_k<BITS, SBT, MT, T, WPB, false, true>(a, grid, lds, MfmaGather{})
-               : launch_k<BITS, SBT, MT, T, WPB, false, false>(a, grid, lds, MfmaGather{});
+    if (sbl) return launch_k<BITS, SBT, MT, T, WPB, false, true>(a, grid, lds, MfmaGather{});
+    // scales and biases read from memory (an odd number of groups per row,
+    // arrays not 4-byte aligned): one tile and four waves per block
+    const dim3 grid1((unsigned)((a.N + 15) / 16));
+    return launch_k<BITS, SBT, MT, 1, 4, false, false>(a, grid1, mfma_lds(a, 1, 4, MT, NMT, &sbl), MfmaGather{});
 }
 
-int pick_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
+constexpr int kSplitBlocks = 256;  // blocks a K split aims at (one per CU)
+constexpr int kMaxGemvSplit = 16;
 
-// tiles per block and waves per block: 16 K-splitting waves once K has at
-// least 64 k-quads (K >= 8192) and M <= 8, else 4; then the most 16-row
-// tiles per block (4, 2 or 1: more tiles amortise the x operand, which every
-// block reads whole from L2) that still give 192 blocks, three quarters of
-// the CUs.  Measured on MI355X with the scales staged in LDS (4-bit g64, us,
-// M = 8 / 16; the choice first): 4096 -> 14336 (T 4) 15.7 / 19.1, T 2 14.9 /
-// 18.9, T 1 18.0 / 23.6; 14336 -> 4096 (T 1, 16 waves) 18.2 / 24.5, four
-// waves 22.4 / 20.6 (hence four at M = 16), T 2 with 16 waves 23.8 / 30.0;
-// 4096 -> 4096 (T 1) 9.1 / 8.9, T 2 10.9 / 11.8.
+// rows of x per MFMA tile: 4, 8 or 16 (M <= 4 reaches this kernel only as a
+// forced route, with the rows past M masked)
+int pick_mt(int64_t M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
+
+// tiles per block and waves per block (unsplit): 8 K-splitting waves once K
+// has at least 64 k-quads (K >= 8192) and M <= 8, else 4; then four 16-row
+// tiles per block where that still gives a block per CU, else two or one
+// where that gives 192 blocks (more tiles amortise the x operand, which every
+// block reads whole).  Measured on MI355X (4-bit g64, us, M = 8 / 16, four
+// waves; the choice first): 4096 -> 14336 (T 2) 13.7 / 18.3, T 4 13.6 /
+// 19.5, T 1 16.6 / 23.6; 4096 -> 6144 (T 2) 8.5 / 12.1, T 1 9.7 / 13.7;
+// 4096 -> 4096 (T 1) 7.3 / 9.4, T 2 8.2 / 11.9; 14336 -> 4096 (T 1) with 8
+// waves 16.0 / 22.8, four 17.2 / 21.4 (with a workspace these split).
 void pick_tw(int64_t M, int64_t N, int64_t K, int bits, int* T, int* WPB) {
     const int64_t KQ = (K / 32 + 3) / 4;
     const int nmt = M > 4 ? (M > 8 ? 4 : 2) : 1;
-    const int wpb = KQ >= 64 && M <= 8 ? 16 : 4;
-    int t = 4;
+    const int wpb = KQ >= 64 && M <= 8 ? 8 : 4;
+    int t = (N + 63) / 64 >= 256 ? 4 : 2;
     while (t > 1 && (N + 16 * t - 1) / (16 * t) < 192) t /= 2;
     while (t > 1 && wpb * t * 64 * nmt * 4 > 32768) t /= 2;  // cross-wave reduction LDS
-    // 16 waves of a block get at most 128 registers each: four tiles' stages
-    // and accumulators do not fit in them (they spilled)
-    if (wpb == 16 && t > 2) t = 2;
+    // four tiles only with four waves (the instantiated kernels)
+    if (wpb == 8 && t > 2) t = 2;
     (void)bits;
     *T = t;
     *WPB = wpb;
@@ -443,7 +607,7 @@ hipError_t launch_w(const QmmArgs& a, int wpb) {
     if constexpr (T == 4) {  // four waves only (pick_tw)
         return launch_t<BITS, SBT, MT, T, 4>(a);
     } else {
-        return wpb == 16 ? launch_t<BITS, SBT, MT, T, 16>(a) : launch_t<BITS, SBT, MT, T, 4>(a);
+        return wpb == 8 ? launch_t<BITS, SBT, MT, T, 8>(a) : launch_t<BITS, SBT, MT, T, 4>(a);
     }
 }
 
@@ -461,7 +625,7 @@ template <int BITS, int SBT, int T, int WPB>
 hipError_t launch_gather_t(const QmmArgs& a, const MfmaGather& g, int64_t max_tiles) {
     constexpr int MT = kGatherGemvRows, NMT = MT / 4;
     const dim3 grid((unsigned)((a.N + 16 * T - 1) / (16 * T)), (unsigned)max_tiles);
-    int sbl = 0;
+    int sbl = 1;
     const size_t lds = mfma_lds(a, T, WPB, MT, NMT, &sbl);
     return sbl ? launch_k<BITS, SBT, MT, T, WPB, true, true>(a, grid, lds, g)
                : launch_k<BITS, SBT, MT, T, WPB, true, false>(a, grid, lds, g);
@@ -479,15 +643,92 @@ hipError_t launch_gather_tw(const QmmArgs& a, const MfmaGather& g, int64_t max_t
 template <int BITS, int SBT>
 hipError_t launch_mt(const QmmArgs& a) {
     switch (pick_mt(a.M)) {
-        case 1: return launch_tt<BITS, SBT, 1>(a);
-        case 2: return launch_tt<BITS, SBT, 2>(a);
         case 4: return launch_tt<BITS, SBT, 4>(a);
         case 8: return launch_tt<BITS, SBT, 8>(a);
         default: return launch_tt<BITS, SBT, 16>(a);
     }
 }
 
+// The K split (a caller workspace holds the partials): blocks of WPB waves
+// own 16 T WPB rows over one of S k ranges each.  Every block reads its
+// range of x once for all its rows; without the split a block reads all of x
+// for at most 64 rows, and at M = 16 that re-read of x from L2 moves more
+// bytes than the codes do (x 2 M bytes per k, the codes K / 2 per row).
+// S brings the blocks to about one per CU.
+struct SplitPlan {
+    int T, WPB, S;
+};
+SplitPlan split_plan(const QmmArgs& a) {
+    SplitPlan p{1, 8, 1};
+    const int mt = pick_mt(a.M);
+    const int cl = cycle_shift(__builtin_ctz((unsigned)a.group_size), 16 / mt);
+    const int64_t KQ = (a.K / 32 + 3) / 4;
+    const int64_t rows = 16 * p.T * p.WPB;
+    const int64_t groups = (a.N + rows - 1) / rows;
+    int64_t S = (kSplitBlocks + groups / 2) / groups;
+    S = S < 1 ? 1 : S > kMaxGemvSplit ? kMaxGemvSplit : S;
+    if (S > 1) {
+        const int64_t qs = wave_kquads((int)a.K, (int)S, cl);
+        S = (KQ + qs - 1) / qs;
+    }
+    p.S = (int)S;
+    return p;
+}
+
+template <int BITS, int SBT, int MT, int T, int WPB>
+hipError_t launch_split_t(const QmmArgs& a, int S, float* part) {
+    const dim3 grid((unsigned)((a.N + 16 * T * WPB - 1) / (16 * T * WPB)), (unsigned)S);
+    const int gsh = __builtin_ctz((unsigned)a.group_size);
+    const int npr = sb_pairs((int)a.K, gsh, S, 16 / MT);
+    const int qs = wave_kquads((int)a.K, S, cycle_shift(gsh, 16 / MT));
+    const size_t lds = (size_t)16 * split_x_stride(qs) + (size_t)WPB * 2 * sb_area_pairs(T, npr) * 4;
+    return launch_k<BITS, SBT, MT, T, WPB, false, true, true>(a, grid, lds, MfmaGather{}, part);
+}
+
+template <int BITS, int SBT, int MT>
+hipError_t launch_split_mt(const QmmArgs& a, const SplitPlan& p, float* part) {
+    (void)p;
+    return launch_split_t<BITS, SBT, MT, 1, 8>(a, p.S, part);
+}
+
+template <int BITS, int SBT>
+hipError_t launch_split(const QmmArgs& a, const SplitPlan& p, float* part) {
+    switch (pick_mt(a.M)) {
+        case 4: return launch_split_mt<BITS, SBT, 4>(a, p, part);
+        case 8: return launch_split_mt<BITS, SBT, 8>(a, p, part);
+        default: return launch_split_mt<BITS, SBT, 16>(a, p, part);
+    }
+}
+
 }  // namespace
+
+// Split where it measured faster (MI355X, 4-bit g64, one tile per wave and
+// eight waves per block against the unsplit kernel's best launch shape, us):
+// K >= 8192 (M = 16: 14336 -> 4096 20.4 -> 15.5; M = 8: 15.0 -> 14.2) and
+// long outputs at M > 8 (M = 16: 4096 -> 14336 18.3 -> 16.1); not at M <= 8
+// with K = 4096 (M = 8: 4096 -> 14336 13.3 unsplit, 14.5 split) nor on
+// 4096 x 4096 (M = 16: 9.2 unsplit, 10.0 split).
+int64_t qmv_split_bytes(const QmmArgs& a) {
+    if (a.M < 1 || a.M > 16 || (a.K / a.group_size) % 2 != 0) return 0;
+    if (a.K < 8192 && !(a.M > 8 && a.N >= 8192)) return 0;
+    const SplitPlan p = split_plan(a);
+    return p.S > 1 ? (int64_t)p.S * a.M * a.N * 4 : 0;
+}
+
+hipError_t launch_qmv_mfma_split(const QmmArgs& a, void* workspace, int64_t workspace_bytes) {
+    const int64_t need = qmv_split_bytes(a);
+    const bool al = ((reinterpret_cast<uintptr_t>(a.scales) | reinterpret_cast<uintptr_t>(a.biases)) & 3) == 0;
+    if (need == 0 || workspace == nullptr || workspace_bytes < need || !al) return launch_qmv_mfma(a);
+    const SplitPlan p = split_plan(a);
+    float* part = static_cast<float*>(workspace);
+    hipError_t e;
+    if (a.bits == 4)
+        e = a.sb_dtype == DT_F16 ? launch_split<4, DT_F16>(a, p, part) : launch_split<4, DT_BF16>(a, p, part);
+    else
+        e = a.sb_dtype == DT_F16 ? launch_split<8, DT_F16>(a, p, part) : launch_split<8, DT_BF16>(a, p, part);
+    if (e != hipSuccess) return e;
+    return launch_split_reduce(part, p.S, a);
+}
 
 void qmv_mfma_config(const QmmArgs& a, int* tiles_per_block, int* m_tile, int* waves_per_block) {
     int T, WPB;

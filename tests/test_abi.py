@@ -244,11 +244,21 @@ def test_query_route(lib):
                                 (256, 4096, 4096): (128, 4), (32, 64, 256): (128, 1)}.items():
         route, tiles = miqmm.query_route(M, N, K, 64, 4)
         assert route == miqmm.ROUTE_QMM and tiles == (256, bn, 64, ks), ((M, N, K), tiles)
-    # the MFMA GEMV's launch shape: the most tiles per block that still give 192 blocks
-    assert miqmm.query_route(8, 14336, 4096, 64, 4)[1] == (4, 8, 4, 0)  # 224 blocks of four tiles
-    # K >= 8192: sixteen K-splitting waves at M <= 8, four at M = 16
-    assert miqmm.query_route(8, 4096, 14336, 64, 4)[1] == (1, 8, 16, 0)
+    # the MFMA GEMV's launch shape (unsplit): four tiles per block where that
+    # gives a block per CU, else two or one where that gives 192 blocks
+    assert miqmm.query_route(8, 14336, 4096, 64, 4)[1] == (2, 8, 4, 0)  # 448 blocks of two tiles
+    assert miqmm.query_route(8, 32768, 4096, 64, 4)[1] == (4, 8, 4, 0)  # 512 blocks of four tiles
+    assert miqmm.query_route(8, 6144, 4096, 64, 4)[1] == (2, 8, 4, 0)
+    # K >= 8192: eight K-splitting waves at M <= 8, four at M = 16
+    assert miqmm.query_route(8, 4096, 14336, 64, 4)[1] == (1, 8, 8, 0)
     assert miqmm.query_route(16, 4096, 14336, 64, 4)[1] == (1, 16, 4, 0)
+    # with a workspace the MFMA GEMV splits K where long rows or a long
+    # output at M > 8 make that faster: S k ranges of fp32 partials
+    for M, N, K in ((16, 4096, 14336), (8, 4096, 14336), (16, 14336, 4096), (5, 512, 8192)):
+        n = miqmm.workspace_size(M, N, K)
+        assert n > 0 and n % (M * N * 4) == 0 and n // (M * N * 4) <= 16, (M, N, K, n)
+    for M, N, K in ((8, 14336, 4096), (16, 4096, 4096), (1, 4096, 14336), (4, 4096, 14336)):
+        assert miqmm.workspace_size(M, N, K) == 0, (M, N, K)
     with pytest.raises(miqmm.MiqmmError) as e:
         miqmm.query_route(1, 64, 96, 64, 4)
     assert e.value.status == miqmm.EINVAL
