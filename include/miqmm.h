@@ -135,9 +135,12 @@ int miqmm_quantized_matmul_ex(void* y, const void* x, const uint32_t* w, const v
 
 /*
  * Bytes of scratch that miqmm_quantized_matmul_ws would use for this shape
- * (the fp32 partials of the tiled matmul's k split: k ranges * M * N * 4
- * when the plan splits the k-steps over several blocks per output tile,
- * which pays when the output tiles are fewer than the CUs, else 0).
+ * (fp32 partials of a k split: k ranges * M * N * 4, else 0).  The tiled
+ * matmul (M > 16) splits its k-steps over several blocks per output tile
+ * when the output tiles are fewer than the CUs; the small-M MFMA GEMV
+ * (5 <= M <= 16) splits K over blocks of 128 rows, each reading its range
+ * of x once, for rows of K >= 8192 codes and, at M > 8, outputs of
+ * N >= 8192.
  * No reference counterpart: the workspace query of the caller that can
  * pass scratch memory.
  */
@@ -148,15 +151,15 @@ int miqmm_quantized_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int g
  * miqmm_quantized_matmul (+ bias when non-null, as miqmm_quantized_linear)
  * with a caller-owned device workspace (16-byte aligned, any contents;
  * NULL / 0 bytes: no split).  With at least
- * miqmm_quantized_matmul_workspace_size bytes the tiled matmul may split
- * the k-steps over several blocks per tile, write fp32 partials there and
- * add them in a second kernel in split order (the same bits for any grid);
+ * miqmm_quantized_matmul_workspace_size bytes the tiled matmul or the small-M
+ * GEMV may split K over several blocks, write fp32 partials there and add
+ * them in a second kernel in split order (the same bits for any grid);
  * with less it runs unsplit, exactly as miqmm_quantized_matmul.  The call
  * only reads and writes the workspace on `stream`: the caller keeps it alive
  * until the work completes (a workspace captured into a graph stays in use
  * by every replay) and must not share it between calls that may overlap.
  * No reference counterpart beyond quantized_matmul itself: the caller that
- * can pass scratch memory for the prefill-sized products.
+ * can pass scratch memory for prefill-sized products and few-row batches.
  */
 int miqmm_quantized_matmul_ws(void* y, const void* x, const uint32_t* w, const void* scales,
                               const void* biases, const void* bias, int64_t M, int64_t N, int64_t K,

@@ -507,8 +507,8 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
 
 // y = sum over z of part[z] (z = 0 .. ks-1 in order, the same bits for any
 // grid), rounded to y's dtype (+ bias as a separate rounding): one thread per
-// run of 4 outputs of a row, four planes' loads in flight at a time (a few
-// rows of x give few threads, each with ks planes to add)
+// run of 4 outputs of a row, all planes' loads in flight at once (a few rows
+// of x give few threads, each with ks planes to add)
 __global__ __launch_bounds__(256) void qmm_split_reduce_kernel(const float* __restrict__ part, int ks, int M, int N,
                                                                void* __restrict__ y, const void* __restrict__ bias,
                                                                int y_dtype) {
@@ -528,17 +528,22 @@ __global__ __launch_bounds__(256) void qmm_split_reduce_kernel(const float* __re
             if (gc + e < N) a[e] = p[e];
         return a;
     };
+    // every plane's load in flight before the first add (ks <= 16 here)
+    constexpr int kPlanes = 16;
+    f32x4_t a[kPlanes];
+#pragma unroll
+    for (int z = 0; z < kPlanes; ++z)
+        if (z < ks) a[z] = ld(z);
     f32x4_t v = {0.f, 0.f, 0.f, 0.f};
-    int z = 0;
-    for (; z + 4 <= ks; z += 4) {
-        const f32x4_t a = ld(z), b = ld(z + 1), c = ld(z + 2), d = ld(z + 3);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (((v[e] + a[e]) + b[e]) + c[e]) + d[e];
-    }
-    for (; z < ks; ++z) {
-        const f32x4_t a = ld(z);
+    for (int z = 0; z < kPlanes; ++z)
+        if (z < ks)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] += a[e];
+            for (int e = 0; e < 4; ++e) v[e] += a[z][e];
+    for (int z = kPlanes; z < ks; ++z) {
+        const f32x4_t b = ld(z);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += b[e];
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e)
