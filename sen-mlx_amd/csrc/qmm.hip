@@ -6,13 +6,15 @@
 // (src/engine/mlx_lm/models/llama.rs:195-197,249,293-294 with x [1, L, K],
 // L up to prefill_chunk; src/engine/mlx_native.rs:1918-1922,2094-2102).
 //
-// Block tile 256 x BN x 64 with four waves in a 2 x 2 grid; each wave owns a
-// 128 x (BN/2) sub-tile computed with v_mfma_f32_32x32x16_bf16 (the
-// accumulators, up to 256 fp32 per lane, live in AGPRs).  A big wave tile
-// keeps LDS reads per MFMA flop low: each 16-wide k step a wave reads 4 A and
-// BN/64 B fragments of 1 KiB for 4*BN/64 MFMAs.
+// Block tile 256 x BN x 64: for BN = 256 (and 8-bit codes) eight waves in a
+// 2 x 4 grid, each a 128 x 64 sub-tile (two waves per SIMD, so one wave's
+// dequant VALU and LDS traffic overlap the other's MFMAs); for 4-bit BN = 128
+// four waves in a 2 x 2 grid, 128 x 64 each (waves_per_block).  Sub-tiles are
+// computed with v_mfma_f32_32x32x16_bf16, the 128 fp32 accumulators per lane
+// in AGPRs; each 16-wide k step a wave reads 4 A and 2 B fragments of 1 KiB
+// for 8 MFMAs.
 //
-// One block per CU, so the pipeline, not other waves, hides memory latency.
+// One block per CU, so the pipeline, not other blocks, hides memory latency.
 // At k-step t the block
 //   - loads the packed codes, scales and biases of step t+2 into registers,
 //   - copies the x tile of step t+2 straight from HBM into a 3-stage LDS ring

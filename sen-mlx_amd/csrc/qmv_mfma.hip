@@ -173,8 +173,10 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
 #endif
     constexpr int kMaxDepth = (63 / kStageLoads) & ~1;  // the loads a vmcnt wait can count
     // SPLIT stages hold only codes: four k-quads in flight (measured on
-    // MI355X, M = 16: 4096 -> 14336 15.5 / 16.2 / 18.2 us with 4 / 8 / 16)
-    constexpr int kDepth = SPLIT ? 4 : QMV_MFMA_DEPTH;
+    // MI355X, M = 16: 14336 -> 4096 15.5 / 16.2 / 18.2 us with 4 / 8 / 16);
+    // unsplit one-tile blocks also take four (M = 8, 4096 -> 4096: 8.9 -> 7.1
+    // us), more tiles two (M = 8, 4096 -> 14336, two tiles: 13.3 -> 15.2)
+    constexpr int kDepth = SPLIT || T == 1 ? 4 : QMV_MFMA_DEPTH;
     constexpr int DEPTH = kDepth < kMaxDepth ? kDepth : kMaxDepth;
     static_assert(DEPTH >= 2 && DEPTH * kStageLoads < 64, "vmcnt range");
 

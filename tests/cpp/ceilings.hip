@@ -11,6 +11,18 @@
 //              copied HBM -> LDS with direct-to-LDS loads (32 per block),
 //              three stages, one wait and barrier per k-step, over the
 //              448 blocks and 64 k-steps of x[2048, 4096] -> N = 14336.
+// and the compute of the two ways to apply the affine dequant, operands in
+// registers (no x or W traffic):
+//   dequant    the matmul's: per 64-wide k-step a wave's 32 MFMAs plus its
+//              share of the W tile (32 codes per lane) dequantized in fp32,
+//              fma(s, q, b), packed to bf16 and stored to LDS; eight waves;
+//   exact      exact integer codes in the MFMA and the dequant applied to the
+//              accumulators: per k-step (one group at g = 64) the 32 MFMAs
+//              start from zero and the group's sums are folded into fp32
+//              totals, tot += s_n D + b'_n X_m (256 fused multiply-adds per
+//              lane, X_m the group sums of x read from LDS), the codes only
+//              unpacked; the second accumulator set leaves room for one wave
+//              per SIMD, four per block.
 // Usage: ceilings [iterations]; prints one line per part.
 #include <hip/hip_runtime.h>
 
@@ -145,6 +157,112 @@ __global__ __launch_bounds__(kThreads) void x_stage(const unsigned short* x, int
     out[(blockIdx.y * gridDim.x + blockIdx.x) * kThreads + threadIdx.x] = s;
 }
 
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)lo, (__bf16)hi});
+}
+
+__global__ __launch_bounds__(kThreads) void dequant(float* out, int iters) {
+    __shared__ u32x4 wst[kThreads * 4];
+    const u32x4 av = {threadIdx.x * 0x10001u, 0x3f803f80u, 0x3f003f00u, threadIdx.x};
+    bf16x8 a[kTM], b[kTN];
+#pragma unroll
+    for (int tm = 0; tm < kTM; ++tm) a[tm] = as_bf16x8(av ^ (0x00010001u * (tm + 1)));
+#pragma unroll
+    for (int tn = 0; tn < kTN; ++tn) b[tn] = as_bf16x8(av ^ (0x00400040u + 0x00020002u * tn));
+    f32x16 acc[kTM * kTN];
+#pragma unroll
+    for (int t = 0; t < kTM * kTN; ++t) acc[t] = f32x16{};
+    uint32_t code = threadIdx.x * 0x9E3779B9u + 1u;
+    float sc = 0.25f + threadIdx.x * 1e-3f, bi = -1.f;
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int t = 0; t < kTM * kTN; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t / kTN], b[t % kTN], acc[t], 0, 0, 0);
+        const u32x4 q = {code, code ^ (uint32_t)i, code + (uint32_t)i, code * 3u};
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) {
+            const uint32_t lo = q[wi] & 0x0F0F0F0Fu, hi = (q[wi] >> 4) & 0x0F0F0F0Fu;
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                o[j] = pack2(fmaf(sc, (float)((lo >> (8 * j)) & 0xFFu), bi), fmaf(sc, (float)((hi >> (8 * j)) & 0xFFu), bi));
+            wst[threadIdx.x * 4 + wi] = o;
+        }
+        code = code * 1664525u + 1013904223u;
+        sc += 1e-7f;
+    }
+    float s = reinterpret_cast<const float*>(wst)[threadIdx.x];
+#pragma unroll
+    for (int t = 0; t < kTM * kTN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s += acc[t][e];
+    out[blockIdx.x * kThreads + threadIdx.x] = s;
+}
+
+constexpr int kExactThreads = 256;  // one wave per SIMD
+__global__ __launch_bounds__(kExactThreads) void exact(float* out, int iters) {
+    __shared__ float xs[64 * 64];  // group sums X_m, 64 groups x 64 rows
+    __shared__ u32x4 wst[kExactThreads * 4];
+    for (int i = threadIdx.x; i < 64 * 64; i += kExactThreads) xs[i] = 1.f + i * 1e-4f;
+    __syncthreads();
+    const u32x4 av = {threadIdx.x * 0x10001u, 0x3f803f80u, 0x3f003f00u, threadIdx.x};
+    bf16x8 a[kTM], b[kTN];  // distinct fragments per tile row and column, as in the matmul
+#pragma unroll
+    for (int tm = 0; tm < kTM; ++tm) a[tm] = as_bf16x8(av ^ (0x00010001u * (tm + 1)));
+#pragma unroll
+    for (int tn = 0; tn < kTN; ++tn) b[tn] = as_bf16x8(av ^ (0x00400040u + 0x00020002u * tn));
+    const int lane = threadIdx.x & 63;
+    float tot[kTM * kTN][16];
+#pragma unroll
+    for (int t = 0; t < kTM * kTN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tot[t][e] = 0.f;
+    uint32_t code = threadIdx.x * 0x9E3779B9u + 1u;
+    for (int i = 0; i < iters; ++i) {
+        f32x16 D[kTM * kTN];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int t = 0; t < kTM * kTN; ++t)
+                D[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[t / kTN], b[t % kTN], kk == 0 ? f32x16{} : D[t], 0,
+                                                               0, 0);
+        // exact codes: 128 + q as bf16 by one and-or per pair
+        const u32x4 q = {code, code ^ (uint32_t)i, code + (uint32_t)i, code * 3u};
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) {
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = ((q[wi] >> (4 * j)) & 0x000F000Fu) | 0x43004300u;
+            wst[threadIdx.x * 4 + wi] = o;
+        }
+        code = code * 1664525u + 1013904223u;
+        // this lane's two output columns' scale and bias, this group's X of its 64 rows
+        const float s0 = 0.25f + (i & 7) * 1e-3f, s1 = s0 + 1e-3f, b0 = -1.f - s0 * 128.f, b1 = -1.f - s1 * 128.f;
+        const float* xg = xs + (i & 63) * 64;
+#pragma unroll
+        for (int tm = 0; tm < kTM; ++tm)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float X = xg[(tm * 16 + e + lane) & 63];
+#pragma unroll
+                for (int tn = 0; tn < kTN; ++tn) {
+                    const int t = tm * kTN + tn;
+                    tot[t][e] = fmaf(tn ? s1 : s0, D[t][e], tot[t][e]);
+                    tot[t][e] = fmaf(tn ? b1 : b0, X, tot[t][e]);
+                }
+            }
+    }
+    float s = reinterpret_cast<const float*>(wst)[threadIdx.x];
+#pragma unroll
+    for (int t = 0; t < kTM * kTN; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s += tot[t][e];
+    out[blockIdx.x * kExactThreads + threadIdx.x] = s;
+}
+
 template <typename F>
 float time_us(hipStream_t st, int reps, F launch) {
     hipEvent_t e0, e1;
@@ -188,6 +306,18 @@ int main(int argc, char** argv) {
     CK(hipGetLastError());
     printf("mfma_lds: %d blocks x 8 waves, %d k-steps (4 A + 2 B fragments, 8 MFMAs per substep): %.1f us, "
            "%.1f TFLOP/s\n", blocks, kiters, us, flop_wave_iter * kWaves * blocks * kiters * 4 / us / 1e6);
+    fflush(stdout);
+
+    const int ksteps = iters / 4;
+    us = time_us(st, 9, [&] { hipLaunchKernelGGL(dequant, dim3(blocks), dim3(kThreads), 0, st, out, ksteps); });
+    CK(hipGetLastError());
+    printf("dequant: %d blocks x 8 waves, %d k-steps (32 MFMAs + 32 codes dequantized per lane): %.1f us, "
+           "%.1f TFLOP/s\n", blocks, ksteps, us, flop_wave_iter * kWaves * blocks * ksteps * 4 / us / 1e6);
+    fflush(stdout);
+    us = time_us(st, 9, [&] { hipLaunchKernelGGL(exact, dim3(blocks), dim3(kExactThreads), 0, st, out, ksteps); });
+    CK(hipGetLastError());
+    printf("exact: %d blocks x 4 waves, %d k-steps (32 MFMAs from zero + 256 fused multiply-adds per lane): %.1f us, "
+           "%.1f TFLOP/s\n", blocks, ksteps, us, flop_wave_iter * 4 * blocks * ksteps * 4 / us / 1e6);
     fflush(stdout);
 
     const int M = 2048, K = 4096, NT = 56;  // N = 14336 in 256-wide tiles
