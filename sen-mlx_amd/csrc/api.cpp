@@ -116,8 +116,13 @@ bool short_rows(int64_t K, int bits) { return K * bits / 128 <= 32; }
 //          MFMA GEMV and 19.3 for v_dot2);
 //   M = 1, other rows: the v_dot2 GEMV, except for many-row heads with K <=
 //          2048, where the LDS-staged MFMA GEMV wins;
-//   2 <= M <= 4: the LDS-staged MFMA GEMV (14336 x 4096: 12.8 / 16.0 us at
-//          M = 2 / 4 against 15.1 / 22.2 us for v_dot2) when it supports the shape;
+//   2 <= M <= 4: the LDS-staged MFMA GEMV (4096 -> 14336: 12.8 / 16.0 us at
+//          M = 2 / 4 against 15.1 / 22.2 us for v_dot2) when it supports the
+//          shape (min(M, 4) K <= 32768), except at M = 3 and 4 with N >= 8192,
+//          where the group-diagonal MFMA GEMV is faster (4096 -> 14336, M = 4:
+//          16.1 -> 13.2 us; at 4096 x 4096 it is slower, 6.6 -> 7.3 us); rows
+//          the LDS-staged GEMV does not take go to the group-diagonal one too
+//          (14336 -> 4096, M = 4, with a workspace: 22.6 us on v_dot2 -> 13.7);
 //   5 <= M <= 16: the group-diagonal MFMA GEMV, whose cost barely grows with M;
 //   larger M: the tiled MFMA matmul.
 int auto_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, bool sb_aligned4 = true) {
@@ -128,7 +133,8 @@ int auto_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, bool s
         const bool wide_head = N >= 65536 && K <= 2048 && miqmm::qmvx_supported(M, K, group_size);
         return wide_head ? MIQMM_ROUTE_QMVX : MIQMM_ROUTE_QMV_DOT;
     }
-    if (M <= 4) return miqmm::qmvx_supported(M, K, group_size) ? MIQMM_ROUTE_QMVX : MIQMM_ROUTE_QMV_DOT;
+    if (M <= 4 && miqmm::qmvx_supported(M, K, group_size) && !(M >= 3 && N >= 8192)) return MIQMM_ROUTE_QMVX;
+    if (M <= 4 && (K / group_size) % 2 != 0) return MIQMM_ROUTE_QMV_DOT;
     return M <= 16 ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
 }
 

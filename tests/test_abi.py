@@ -229,8 +229,13 @@ def test_query_route(lib):
     route, tiles = miqmm.query_route(2, 151936, 896, 64, 4)
     assert route == miqmm.ROUTE_QMVX and tiles[0] == 2
     for M, mt in ((2, 2), (3, 4), (4, 4)):
-        route, tiles = miqmm.query_route(M, 14336, 4096, 64, 4)
+        route, tiles = miqmm.query_route(M, 4096, 4096, 64, 4)
         assert route == miqmm.ROUTE_QMVX and tiles[0] == mt and tiles[1] in (1, 2, 4)
+    # ... except M = 3 and 4 with long outputs, and rows it does not take
+    # (min(M, 4) K > 32768): the group-diagonal MFMA GEMV
+    assert miqmm.query_route(2, 14336, 4096, 64, 4)[0] == miqmm.ROUTE_QMVX
+    for M, N, K in ((3, 14336, 4096), (4, 14336, 4096), (3, 4096, 14336), (4, 4096, 14336)):
+        assert miqmm.query_route(M, N, K, 64, 4)[0] == miqmm.ROUTE_QMV, (M, N, K)
     # qmvx needs an even number of groups per row: K = 96, g = 32 falls back to v_dot2
     assert miqmm.query_route(2, 128, 96, 32, 4)[0] == miqmm.ROUTE_QMV_DOT
     for M in (5, 8, 16):
@@ -254,10 +259,10 @@ def test_query_route(lib):
     assert miqmm.query_route(16, 4096, 14336, 64, 4)[1] == (1, 16, 4, 0)
     # with a workspace the MFMA GEMV splits K where long rows or a long
     # output at M > 8 make that faster: S k ranges of fp32 partials
-    for M, N, K in ((16, 4096, 14336), (8, 4096, 14336), (16, 14336, 4096), (5, 512, 8192)):
+    for M, N, K in ((16, 4096, 14336), (8, 4096, 14336), (16, 14336, 4096), (5, 512, 8192), (4, 4096, 14336)):
         n = miqmm.workspace_size(M, N, K)
         assert n > 0 and n % (M * N * 4) == 0 and n // (M * N * 4) <= 16, (M, N, K, n)
-    for M, N, K in ((8, 14336, 4096), (16, 4096, 4096), (1, 4096, 14336), (4, 4096, 14336)):
+    for M, N, K in ((8, 14336, 4096), (16, 4096, 4096), (1, 4096, 14336), (2, 4096, 14336), (4, 14336, 4096)):
         assert miqmm.workspace_size(M, N, K) == 0, (M, N, K)
     with pytest.raises(miqmm.MiqmmError) as e:
         miqmm.query_route(1, 64, 96, 64, 4)
