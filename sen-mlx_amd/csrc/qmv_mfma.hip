@@ -468,7 +468,8 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
     }
 
     if constexpr (SPLIT) {
-        // this wave's partial sums of its range: lane (nl, q) holds m = q NMT + i of row n0 + 16 t + nl
+        // lane (nl, q) holds m = q NMT + i of row n0 + 16 t + nl: this wave's
+        // partial sums of its range, or with one range the outputs
         float* const part = static_cast<float*>(y) + (size_t)blockIdx.y * M * N;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
@@ -476,7 +477,9 @@ __global__ __launch_bounds__(WPB * 64) void qmv_mfma_kernel(const uint16_t* __re
 #pragma unroll
             for (int i = 0; i < NMT; ++i) {
                 const int m = q * NMT + i;
-                if (m < M && n < N) part[(size_t)m * N + n] = tot[t][i];
+                if (m >= M || n >= N) continue;
+                if (ksplit == 1) store_out(y, (int64_t)m * N + n, y_dtype, tot[t][i], bias, n);
+                else part[(size_t)m * N + n] = tot[t][i];
             }
         }
         return;
@@ -542,9 +545,10 @@ hipError_t launch_kc(const QmmArgs& a, dim3 grid, size_t lds, const MfmaGather& 
     constexpr auto kernel = qmv_mfma_kernel<BITS, SBT, MT, T, WPB, GATHER, SBL, CLS, SPLIT>;
     const hipError_t e = allow_lds<kernel>(lds);
     if (e != hipSuccess) return e;
+    // SPLIT with one k range (part == nullptr) writes y itself
     hipLaunchKernelGGL(kernel, grid, dim3(WPB * 64), lds, a.stream, (const uint16_t*)a.x, a.w,
-                       (const uint16_t*)a.scales, (const uint16_t*)a.biases, SPLIT ? (void*)part : a.y,
-                       GATHER || SPLIT ? nullptr : a.bias, GATHER ? MT : (int)a.M, (int)a.N, (int)a.K,
+                       (const uint16_t*)a.scales, (const uint16_t*)a.biases, part ? (void*)part : a.y,
+                       GATHER || part ? nullptr : a.bias, GATHER ? MT : (int)a.M, (int)a.N, (int)a.K,
                        __builtin_ctz((unsigned)a.group_size), a.y_dtype, (int)grid.y, g);
     return hipGetLastError();
 }
@@ -657,6 +661,15 @@ hipError_t launch_mt(const QmmArgs& a) {
 // for at most 64 rows, and at M = 16 that re-read of x from L2 moves more
 // bytes than the codes do (x 2 M bytes per k, the codes K / 2 per row).
 // S brings the blocks to about one per CU.
+// LDS of a split launch: the block's A rows of x over its k range, then the
+// waves' scale / bias areas
+size_t split_lds(const QmmArgs& a, int T, int WPB, int MT, int S) {
+    const int gsh = __builtin_ctz((unsigned)a.group_size);
+    const int npr = sb_pairs((int)a.K, gsh, S, 16 / MT);
+    const int qs = wave_kquads((int)a.K, S, cycle_shift(gsh, 16 / MT));
+    return (size_t)16 * split_x_stride(qs) + (size_t)WPB * 2 * sb_area_pairs(T, npr) * 4;
+}
+
 struct SplitPlan {
     int T, WPB, S;
 };
@@ -669,9 +682,18 @@ SplitPlan split_plan(const QmmArgs& a) {
     const int64_t groups = (a.N + rows - 1) / rows;
     int64_t S = (kSplitBlocks + groups / 2) / groups;
     S = S < 1 ? 1 : S > kMaxGemvSplit ? kMaxGemvSplit : S;
-    if (S > 1) {
-        const int64_t qs = wave_kquads((int)a.K, (int)S, cl);
-        S = (KQ + qs - 1) / qs;
+    // more ranges where a range's x and scales would not fit the LDS
+    for (int64_t s = S; S > 1; ++s) {
+        if (s > kMaxGemvSplit) {
+            S = 1;
+            break;
+        }
+        const int64_t qs = wave_kquads((int)a.K, (int)s, cl);
+        const int64_t se = (KQ + qs - 1) / qs;
+        if (split_lds(a, p.T, p.WPB, mt, (int)se) <= 160 * 1024) {
+            S = se;
+            break;
+        }
     }
     p.S = (int)S;
     return p;
@@ -680,11 +702,8 @@ SplitPlan split_plan(const QmmArgs& a) {
 template <int BITS, int SBT, int MT, int T, int WPB>
 hipError_t launch_split_t(const QmmArgs& a, int S, float* part) {
     const dim3 grid((unsigned)((a.N + 16 * T * WPB - 1) / (16 * T * WPB)), (unsigned)S);
-    const int gsh = __builtin_ctz((unsigned)a.group_size);
-    const int npr = sb_pairs((int)a.K, gsh, S, 16 / MT);
-    const int qs = wave_kquads((int)a.K, S, cycle_shift(gsh, 16 / MT));
-    const size_t lds = (size_t)16 * split_x_stride(qs) + (size_t)WPB * 2 * sb_area_pairs(T, npr) * 4;
-    return launch_k<BITS, SBT, MT, T, WPB, false, true, true>(a, grid, lds, MfmaGather{}, part);
+    return launch_k<BITS, SBT, MT, T, WPB, false, true, true>(a, grid, split_lds(a, T, WPB, MT, S), MfmaGather{},
+                                                              part);
 }
 
 template <int BITS, int SBT, int MT>
@@ -755,6 +774,16 @@ hipError_t launch_gather_gemv(const QmmArgs& a, const int32_t* idx, int64_t T, i
 }
 
 hipError_t launch_qmv_mfma(const QmmArgs& a) {
+    // long outputs (a block per CU or more at 128 rows per block): the
+    // row-split blocks with one k range, x staged once per 128 rows
+    const bool al = ((reinterpret_cast<uintptr_t>(a.scales) | reinterpret_cast<uintptr_t>(a.biases)) & 3) == 0;
+    if (a.M >= 5 && a.N >= 128 * kSplitBlocks && (a.K / a.group_size) % 2 == 0 && al &&
+        split_lds(a, 1, 8, pick_mt(a.M), 1) <= 160 * 1024) {
+        const SplitPlan p{1, 8, 1};
+        if (a.bits == 4)
+            return a.sb_dtype == DT_F16 ? launch_split<4, DT_F16>(a, p, nullptr) : launch_split<4, DT_BF16>(a, p, nullptr);
+        return a.sb_dtype == DT_F16 ? launch_split<8, DT_F16>(a, p, nullptr) : launch_split<8, DT_BF16>(a, p, nullptr);
+    }
     if (a.bits == 4)
         return a.sb_dtype == DT_F16 ? launch_mt<4, DT_F16>(a) : launch_mt<4, DT_BF16>(a);
     return a.sb_dtype == DT_F16 ? launch_mt<8, DT_F16>(a) : launch_mt<8, DT_BF16>(a);
