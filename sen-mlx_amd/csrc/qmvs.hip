@@ -264,8 +264,11 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
         q[j] = bload16_nt(wr, cv ? (uint32_t)(rh + j) * row_bytes + (uint32_t)c * 16 : kOOB);
     // the row this lane stores: row t of the block by lane t of wave 0, into
     // its problem's output (and with its bias)
-    const int t_row = lane;
-    const bool t_mine = ws == 0 && lane < nrows;
+    // (one slice per row: the lanes that end the wave's reduction holding a
+    // row's sum store it, lane (64 / RB) t for row t, with no trip through LDS)
+    const bool one = KS == 1;
+    const int t_row = one ? lane / (64 / RB) : lane;
+    const bool t_mine = one ? (lane & (64 / RB - 1)) == 0 && t_row < nrows : ws == 0 && lane < nrows;
     const int t_glob = r0 + t_row;
     const int t_p = (t_glob >= grp.row0[0]) + (t_glob >= grp.row0[1]) + (t_glob >= grp.row0[2]);
     const size_t t_off = (size_t)(t_glob - (t_p == 0 ? 0 : grp.row0[t_p - 1])) * ysz;
@@ -393,17 +396,22 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     float tot;
     if constexpr (HALF) tot = transposed_sum32<RB>(part, lane);
     else tot = transposed_sum<RB>(part, lane);
-    // the slice partials meet in LDS; row t is summed (slices in order) and
-    // stored by lane t of wave 0
-    float* const kp = reinterpret_cast<float*>(smem + KS * wave_lds<ND>());
-    if ((lane & (64 / RB - 1)) == 0) kp[ws * RB + lane / (64 / RB)] = tot;
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (!t_mine) return;
     float v = 0.f;
-    for (int w = 0; w < KS; ++w) v += kp[w * RB + t_row];
+    if (one) {
+        if (!t_mine) return;
+        v += tot;
+    } else {
+        // the slice partials meet in LDS; row t is summed (slices in order)
+        // and stored by lane t of wave 0
+        float* const kp = reinterpret_cast<float*>(smem + KS * wave_lds<ND>());
+        if ((lane & (64 / RB - 1)) == 0) kp[ws * RB + lane / (64 / RB)] = tot;
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (!t_mine) return;
+        for (int w = 0; w < KS; ++w) v += kp[w * RB + t_row];
+    }
     // plain stores (measured on MI355X: a non-temporal store per block added
     // 3.5 us to a 6 us streaming read)
     char* const ya = (t_p == 0 ? (char*)P.y : (char*)grp.y[t_p - 1]) + t_off;
