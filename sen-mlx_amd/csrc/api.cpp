@@ -116,6 +116,9 @@ bool short_rows(int64_t K, int bits) { return K * bits / 128 <= 32; }
 //          MFMA GEMV and 19.3 for v_dot2);
 //   M = 1, other rows: the v_dot2 GEMV, except for many-row heads with K <=
 //          2048, where the LDS-staged MFMA GEMV wins;
+//   M = 2, K >= 2048: the K-sliced GEMV with both rows of x per row of codes
+//          (4096 -> 14336 10.5 us against 12.3 for the LDS-staged MFMA GEMV;
+//          4096 -> 6144 5.7 against 7.8; on rows of 896 it is slower);
 //   2 <= M <= 4: the LDS-staged MFMA GEMV (4096 -> 14336: 12.8 / 16.0 us at
 //          M = 2 / 4 against 15.1 / 22.2 us for v_dot2) when it supports the
 //          shape (min(M, 4) K <= 32768), except at M = 3 and 4 with N >= 8192,
@@ -128,6 +131,8 @@ bool short_rows(int64_t K, int bits) { return K * bits / 128 <= 32; }
 int auto_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, bool sb_aligned4 = true) {
     if (M == 1 && (K >= kMinSlicedK || short_rows(K, bits)) && sb_aligned4 &&
         miqmm::qmvs_supported(M, N, K, bits, group_size))
+        return MIQMM_ROUTE_QMVS;
+    if (M == 2 && K >= kMinSlicedK && sb_aligned4 && miqmm::qmvs_supported(M, N, K, bits, group_size))
         return MIQMM_ROUTE_QMVS;
     if (M == 1) {
         const bool wide_head = N >= 65536 && K <= 2048 && miqmm::qmvx_supported(M, K, group_size);
@@ -155,8 +160,8 @@ int check_args(void* y, const void* x, const uint32_t* w, const void* scales, co
     if (route != MIQMM_ROUTE_AUTO && route != MIQMM_ROUTE_QMV && route != MIQMM_ROUTE_QMM &&
         route != MIQMM_ROUTE_QMV_DOT && route != MIQMM_ROUTE_QMVX && route != MIQMM_ROUTE_QMVS)
         return fail(MIQMM_EINVAL, "route %d invalid", route);
-    if (route == MIQMM_ROUTE_QMVS && M > 1)
-        return fail(MIQMM_ENOTSUP, "route qmvs takes one row of x (M <= 1)");
+    if (route == MIQMM_ROUTE_QMVS && M > 2)
+        return fail(MIQMM_ENOTSUP, "route qmvs takes one or two rows of x (M <= 2)");
     if (route == MIQMM_ROUTE_QMVS && !miqmm::qmvs_supported(1, N, K, bits, group_size))
         return fail(MIQMM_ENOTSUP, "route qmvs needs K*bits/8 <= 15 KiB and an even K/group_size");
     if (route == MIQMM_ROUTE_QMVS && M > 0 && (!aligned4(scales) || !aligned4(biases)))

@@ -188,7 +188,11 @@ constexpr int max_threads() { return RB >= 32 ? 512 : 1024; }  // 32 rows of cod
 // different rows, lanes 32h .. 32h + 31 the rows h RB/2 .. h RB/2 + RB/2 - 1
 // of the block, so no lane idles past a short row's end (K = 896 at 4 bits
 // is 28 chunks); the reduction starts from its 32-lane state.
-template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF>
+//
+// MX rows of x (1 or 2): each row of codes is unpacked once and dotted with
+// every row of x; the wave reduces RB * MX sums (value m * RB + j, or with
+// HALF m * RB/2 + j in each half).
+template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF, int MX>
 __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t* xp, const uint32_t* wp,
                                                                  const uint16_t* sp, const uint16_t* bp, int n, int k,
                                                                  uint32_t meta, void* yp, const void* biasp,
@@ -216,19 +220,22 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     const int nrows = min(RB, P.N - r0);
     constexpr int ysz = YF32 ? 4 : 2;
 
-    // x chunk of this lane (zero past the row end); prepared below, once the
-    // codes are in flight
-    uint32_t xw[NP];
+    constexpr int RV = RB * MX;  // sums the wave reduces
+    // x chunk of this lane in each row of x (zero past the row end); prepared
+    // below, once the codes are in flight
+    uint32_t xw[MX][NP];
     {
-        const auto xr = make_rsrc(P.x, (uint32_t)K * 2);
+        const auto xr = make_rsrc(P.x, (uint32_t)(MX * K) * 2);
 #pragma unroll
-        for (int i = 0; i < XQ; ++i) {
-            const u32x4_t v = bload16(xr, cv ? (uint32_t)c * CPC * 2 + i * 16 : kOOB);
-            xw[4 * i + 0] = v[0];
-            xw[4 * i + 1] = v[1];
-            xw[4 * i + 2] = v[2];
-            xw[4 * i + 3] = v[3];
-        }
+        for (int m = 0; m < MX; ++m)
+#pragma unroll
+            for (int i = 0; i < XQ; ++i) {
+                const u32x4_t v = bload16(xr, cv ? (uint32_t)(m * K + c * CPC) * 2 + i * 16 : kOOB);
+                xw[m][4 * i + 0] = v[0];
+                xw[m][4 * i + 1] = v[1];
+                xw[m][4 * i + 2] = v[2];
+                xw[m][4 * i + 3] = v[3];
+            }
     }
 
     // The loads are issued in this order, fenced against the scheduler: the
@@ -266,12 +273,15 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     // its problem's output (and with its bias)
     // (one slice per row: the lanes that end the wave's reduction holding a
     // row's sum store it, lane (64 / RB) t for row t, with no trip through LDS)
+    // (the value a lane stores: t_v, of row of x t_m and row of the block t_row)
     const bool one = KS == 1;
-    const int t_row = one ? lane / (64 / RB) : lane;
-    const bool t_mine = one ? (lane & (64 / RB - 1)) == 0 && t_row < nrows : ws == 0 && lane < nrows;
+    const int t_v = one ? lane / (64 / RV) : lane;
+    const int t_m = HALF ? (t_v % (RV / 2)) / (RB / 2) : t_v / RB;
+    const int t_row = HALF ? (t_v / (RV / 2)) * (RB / 2) + t_v % (RB / 2) : t_v % RB;
+    const bool t_mine = one ? (lane & (64 / RV - 1)) == 0 && t_row < nrows : ws == 0 && t_v < RV && t_row < nrows;
     const int t_glob = r0 + t_row;
     const int t_p = (t_glob >= grp.row0[0]) + (t_glob >= grp.row0[1]) + (t_glob >= grp.row0[2]);
-    const size_t t_off = (size_t)(t_glob - (t_p == 0 ? 0 : grp.row0[t_p - 1])) * ysz;
+    const size_t t_off = ((size_t)t_m * P.N + (size_t)(t_glob - (t_p == 0 ? 0 : grp.row0[t_p - 1]))) * ysz;
     uint32_t bias_bits = 0;
     if constexpr (BIAS) {  // every lane loads (a lane past the rows reads row 0's): one load, counted below
         const char* const bp0 = t_p == 0 ? (const char*)P.bias : (const char*)grp.bias[t_p - 1];
@@ -282,50 +292,56 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
 
     __builtin_amdgcn_sched_barrier(0);
     // x prepared: pairs (x_j, x_{j+4}) matching the 4-bit unpack, and the sum
-    uint32_t X[NP];
-    float xs = 0.f;
-#pragma unroll
-    for (int i = 0; i < NP; ++i) xs = dot2(xw[i], kOnesBf16x2, xs);
+    uint32_t X[MX][NP];
+    float xs[MX];
 #if QMVS_F16
-    // fp16 operands: x scaled by 2^-E (E: exponent of the chunk's largest
-    // |x|, so every operand is below 2 and exact unless below fp16's normal
-    // range), the operands facing the codes taken at bits 4-7 further by
-    // 1/16; xsc = 2^E and xoff = -2^E * 1024 * (sum of the operands) undo
-    // the scale and the codes' 1024 offset
-    float xsc, xoff;
-    if constexpr (BITS == 4) {
-        uint32_t emax = 0;
-#pragma unroll
-        for (int i = 0; i < NP; ++i) emax = max(emax, max((xw[i] >> 7) & 0xFFu, (xw[i] >> 23) & 0xFFu));
-        const int e = (int)emax - 127;
-        xsc = __builtin_amdgcn_ldexpf(1.f, e);
-        auto h = [&](int k, int extra) {  // x_k of the chunk, scaled, as fp16 bits
-            const uint32_t w = xw[k >> 1];
-            const float f = __uint_as_float((k & 1) ? (w & 0xFFFF0000u) : (w << 16));
-            return (uint32_t)f32_to_f16_bits(__builtin_amdgcn_ldexpf(f, -e - extra));
-        };
-        float ssum = 0.f;
-#pragma unroll
-        for (int wi = 0; wi < 4; ++wi) {
-            const int k0 = 8 * wi;
-            X[4 * wi + 0] = h(k0 + 0, 0) | (h(k0 + 4, 0) << 16);
-            X[4 * wi + 1] = h(k0 + 1, 4) | (h(k0 + 5, 4) << 16);
-            X[4 * wi + 2] = h(k0 + 2, 0) | (h(k0 + 6, 0) << 16);
-            X[4 * wi + 3] = h(k0 + 3, 4) | (h(k0 + 7, 4) << 16);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                ssum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, X[4 * wi + t]),
-                                              __builtin_bit_cast(half2_t, 0x3C003C00u), ssum, false);
-        }
-        xoff = -xsc * 1024.f * ssum;
-    } else
+    float xsc[MX], xoff[MX];
 #endif
-    if constexpr (BITS == 4) {
 #pragma unroll
-        for (int wi = 0; wi < 4; ++wi) perm_x_for4(&xw[4 * wi], &X[4 * wi]);
-    } else {
+    for (int m = 0; m < MX; ++m) {
+        xs[m] = 0.f;
 #pragma unroll
-        for (int i = 0; i < NP; ++i) X[i] = xw[i];
+        for (int i = 0; i < NP; ++i) xs[m] = dot2(xw[m][i], kOnesBf16x2, xs[m]);
+#if QMVS_F16
+        // fp16 operands: x scaled by 2^-E (E: exponent of the chunk's largest
+        // |x|, so every operand is below 2 and exact unless below fp16's normal
+        // range), the operands facing the codes taken at bits 4-7 further by
+        // 1/16; xsc = 2^E and xoff = -2^E * 1024 * (sum of the operands) undo
+        // the scale and the codes' 1024 offset
+        if constexpr (BITS == 4) {
+            uint32_t emax = 0;
+#pragma unroll
+            for (int i = 0; i < NP; ++i) emax = max(emax, max((xw[m][i] >> 7) & 0xFFu, (xw[m][i] >> 23) & 0xFFu));
+            const int e = (int)emax - 127;
+            xsc[m] = __builtin_amdgcn_ldexpf(1.f, e);
+            auto h = [&](int k, int extra) {  // x_k of the chunk, scaled, as fp16 bits
+                const uint32_t w = xw[m][k >> 1];
+                const float f = __uint_as_float((k & 1) ? (w & 0xFFFF0000u) : (w << 16));
+                return (uint32_t)f32_to_f16_bits(__builtin_amdgcn_ldexpf(f, -e - extra));
+            };
+            float ssum = 0.f;
+#pragma unroll
+            for (int wi = 0; wi < 4; ++wi) {
+                const int k0 = 8 * wi;
+                X[m][4 * wi + 0] = h(k0 + 0, 0) | (h(k0 + 4, 0) << 16);
+                X[m][4 * wi + 1] = h(k0 + 1, 4) | (h(k0 + 5, 4) << 16);
+                X[m][4 * wi + 2] = h(k0 + 2, 0) | (h(k0 + 6, 0) << 16);
+                X[m][4 * wi + 3] = h(k0 + 3, 4) | (h(k0 + 7, 4) << 16);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    ssum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, X[m][4 * wi + t]),
+                                                  __builtin_bit_cast(half2_t, 0x3C003C00u), ssum, false);
+            }
+            xoff[m] = -xsc[m] * 1024.f * ssum;
+        } else
+#endif
+        if constexpr (BITS == 4) {
+#pragma unroll
+            for (int wi = 0; wi < 4; ++wi) perm_x_for4(&xw[m][4 * wi], &X[m][4 * wi]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NP; ++i) X[m][i] = xw[m][i];
+        }
     }
 
     // the DMA must land before the stage is read from LDS (the compiler does
@@ -345,12 +361,11 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     // the row end (if any), lanes past it take zero scales and biases, so
     // they add nothing whatever their LDS holds
     const bool partial = __builtin_amdgcn_readfirstlane((int)(ws == KS - 1 && (C & 63) != 0)) != 0;
-    float part[RL];
+    float part[RL * MX];  // value m * RL + j
     auto rows = [&](auto masked) {
 #pragma unroll
         for (int j = 0; j < RL; ++j) {
             uint32_t p[NP];
-            float a = 0.f;
             const int jr = rh + j;  // row of the block
             float s = half_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(wl + jr * sb + sl_off));
             float b = half_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(wl + ND * kSliceBytes + jr * sb + sl_off));
@@ -370,10 +385,14 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
                     p[4 * wi + 3] = and_or(w8, kMaskHi, kMagic1024);
                 }
 #pragma unroll
-                for (int i = 0; i < NP; ++i)
-                    a = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, X[i]), __builtin_bit_cast(half2_t, p[i]),
-                                               a, false);
-                part[j] = fmaf(s, fmaf(a, xsc, xoff), b * xs);
+                for (int m = 0; m < MX; ++m) {
+                    float a = 0.f;
+#pragma unroll
+                    for (int i = 0; i < NP; ++i)
+                        a = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, X[m][i]),
+                                                   __builtin_bit_cast(half2_t, p[i]), a, false);
+                    part[m * RL + j] = fmaf(s, fmaf(a, xsc[m], xoff[m]), b * xs[m]);
+                }
                 continue;
             }
 #endif
@@ -382,10 +401,14 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
                 if constexpr (BITS == 4) unpack4_magic(q[j][wi], &p[wi * 4], kMask, kMagic);
                 else unpack8_pairs(q[j][wi], &p[wi * 2]);
             }
-#pragma unroll
-            for (int i = 0; i < NP; ++i) a = dot2(X[i], p[i], a);
             if constexpr (BITS == 4) b = fmaf(-128.f, s, b);
-            part[j] = fmaf(b, xs, s * a);
+#pragma unroll
+            for (int m = 0; m < MX; ++m) {
+                float a = 0.f;
+#pragma unroll
+                for (int i = 0; i < NP; ++i) a = dot2(X[m][i], p[i], a);
+                part[m * RL + j] = fmaf(b, xs[m], s * a);
+            }
         }
     };
     // always masked: a uniform branch to an unmasked copy for full slices
@@ -394,8 +417,8 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     rows(std::true_type{});
     // the wave's sum of row j lands in lanes (64 / RB) j .. (64 / RB) (j + 1) - 1
     float tot;
-    if constexpr (HALF) tot = transposed_sum32<RB>(part, lane);
-    else tot = transposed_sum<RB>(part, lane);
+    if constexpr (HALF) tot = transposed_sum32<RV>(part, lane);
+    else tot = transposed_sum<RV>(part, lane);
     float v = 0.f;
     if (one) {
         if (!t_mine) return;
@@ -404,13 +427,13 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
         // the slice partials meet in LDS; row t is summed (slices in order)
         // and stored by lane t of wave 0
         float* const kp = reinterpret_cast<float*>(smem + KS * wave_lds<ND>());
-        if ((lane & (64 / RB - 1)) == 0) kp[ws * RB + lane / (64 / RB)] = tot;
+        if ((lane & (64 / RV - 1)) == 0) kp[ws * RV + lane / (64 / RV)] = tot;
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (!t_mine) return;
-        for (int w = 0; w < KS; ++w) v += kp[w * RB + t_row];
+        for (int w = 0; w < KS; ++w) v += kp[w * RV + t_v];
     }
     // plain stores (measured on MI355X: a non-temporal store per block added
     // 3.5 us to a 6 us streaming read)
@@ -451,13 +474,13 @@ int rows_per_block(int64_t N, int ks) {
     return 4;
 }
 
-template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF>
+template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF, int MX>
 hipError_t launch_t(const QmmArgs& a, const QmvsGroup& g, int ks) {
     const QmvsArgs P{(const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y, a.bias,
                      (int)a.N, (int)a.K, __builtin_ctz((unsigned)a.group_size), a.y_dtype};
-    const size_t lds = (size_t)ks * wave_lds<ND>() + (size_t)ks * RB * 4;
+    const size_t lds = (size_t)ks * wave_lds<ND>() + (size_t)ks * RB * MX * 4;
     const int blocks = (int)((a.N + RB - 1) / RB);
-    hipLaunchKernelGGL((qmvs_kernel<BITS, SBT, RB, ND, YF32, BIAS, HALF>), dim3(blocks), dim3(64 * ks), lds, a.stream, P.x,
+    hipLaunchKernelGGL((qmvs_kernel<BITS, SBT, RB, ND, YF32, BIAS, HALF, MX>), dim3(blocks), dim3(64 * ks), lds, a.stream, P.x,
                        P.w, P.s, P.b, P.N, P.K, (uint32_t)P.gs_shift | (uint32_t)P.y_dtype << 8 | (uint32_t)ks << 16, P.y,
                        P.bias, g);
     return hipGetLastError();
@@ -466,43 +489,54 @@ hipError_t launch_t(const QmmArgs& a, const QmvsGroup& g, int ks) {
 // rows of at most 32 chunks in one slice: the half-wave rows
 bool half_rows(int64_t K, int bits) { return slices(K, bits) == 1 && K * bits / 128 <= 32; }
 
-template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS>
+template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, int MX>
 hipError_t launch_h(const QmmArgs& a, const QmvsGroup& g, int ks) {
-    return half_rows(a.K, BITS) ? launch_t<BITS, SBT, RB, ND, YF32, BIAS, true>(a, g, ks)
-                                : launch_t<BITS, SBT, RB, ND, YF32, BIAS, false>(a, g, ks);
+    return half_rows(a.K, BITS) ? launch_t<BITS, SBT, RB, ND, YF32, BIAS, true, MX>(a, g, ks)
+                                : launch_t<BITS, SBT, RB, ND, YF32, BIAS, false, MX>(a, g, ks);
 }
 
-template <int BITS, int SBT, int RB, bool YF32, bool BIAS>
+template <int BITS, int SBT, int RB, bool YF32, bool BIAS, int MX>
 hipError_t launch_nd(const QmmArgs& a, const QmvsGroup& g, int ks) {
     // bytes of scales per row and slice: (1 KiB of codes / group) * 2
     const int sb = 2 * ((kSliceBytes * 8 / BITS) / a.group_size);
-    if (RB * sb > 2 * kSliceBytes) return launch_h<BITS, SBT, RB, 4, YF32, BIAS>(a, g, ks);
-    if (RB * sb > kSliceBytes) return launch_h<BITS, SBT, RB, 2, YF32, BIAS>(a, g, ks);
-    return launch_h<BITS, SBT, RB, 1, YF32, BIAS>(a, g, ks);
+    if (RB * sb > 2 * kSliceBytes) return launch_h<BITS, SBT, RB, 4, YF32, BIAS, MX>(a, g, ks);
+    if (RB * sb > kSliceBytes) return launch_h<BITS, SBT, RB, 2, YF32, BIAS, MX>(a, g, ks);
+    return launch_h<BITS, SBT, RB, 1, YF32, BIAS, MX>(a, g, ks);
 }
 
-template <int BITS, int SBT, bool YF32, bool BIAS>
+template <int BITS, int SBT, bool YF32, bool BIAS, int MX>
 hipError_t launch_rb(const QmmArgs& a, const QmvsGroup& g) {
     const int ks = slices(a.K, BITS);
     switch (rows_per_block(a.N, ks)) {
-        case 32: return launch_nd<BITS, SBT, 32, YF32, BIAS>(a, g, ks);
-        case 16: return launch_nd<BITS, SBT, 16, YF32, BIAS>(a, g, ks);
-        case 8: return launch_nd<BITS, SBT, 8, YF32, BIAS>(a, g, ks);
-        default: return launch_nd<BITS, SBT, 4, YF32, BIAS>(a, g, ks);
+#if QMVS_RB_FORCE == 32
+        case 32: return launch_nd<BITS, SBT, 32, YF32, BIAS, 1>(a, g, ks);
+#endif
+        case 16: return launch_nd<BITS, SBT, 16, YF32, BIAS, MX>(a, g, ks);
+        case 8: return launch_nd<BITS, SBT, 8, YF32, BIAS, MX>(a, g, ks);
+        default: return launch_nd<BITS, SBT, 4, YF32, BIAS, MX>(a, g, ks);
     }
 }
 
-template <bool YF32, bool BIAS>
+template <bool YF32, bool BIAS, int MX>
 hipError_t launch_y(const QmmArgs& a, const QmvsGroup& g) {
     if (a.bits == 4)
-        return a.sb_dtype == DT_F16 ? launch_rb<4, DT_F16, YF32, BIAS>(a, g) : launch_rb<4, DT_BF16, YF32, BIAS>(a, g);
-    return a.sb_dtype == DT_F16 ? launch_rb<8, DT_F16, YF32, BIAS>(a, g) : launch_rb<8, DT_BF16, YF32, BIAS>(a, g);
+        return a.sb_dtype == DT_F16 ? launch_rb<4, DT_F16, YF32, BIAS, MX>(a, g)
+                                    : launch_rb<4, DT_BF16, YF32, BIAS, MX>(a, g);
+    return a.sb_dtype == DT_F16 ? launch_rb<8, DT_F16, YF32, BIAS, MX>(a, g)
+                                : launch_rb<8, DT_BF16, YF32, BIAS, MX>(a, g);
 }
 
+template <int MX>
+hipError_t launch_m(const QmmArgs& a, const QmvsGroup& g) {
+    if (a.y_dtype == DT_F32) return a.bias ? launch_y<true, true, MX>(a, g) : launch_y<true, false, MX>(a, g);
+    return a.bias ? launch_y<false, true, MX>(a, g) : launch_y<false, false, MX>(a, g);
+}
+
+// one or two rows of x (two: no grouped problems)
 hipError_t launch_g(const QmmArgs& a, const QmvsGroup& g) {
-    if (a.M != 1) return hipErrorInvalidValue;
-    if (a.y_dtype == DT_F32) return a.bias ? launch_y<true, true>(a, g) : launch_y<true, false>(a, g);
-    return a.bias ? launch_y<false, true>(a, g) : launch_y<false, false>(a, g);
+    if (a.M == 1) return launch_m<1>(a, g);
+    if (a.M == 2 && g.row0[0] == INT_MAX) return launch_m<2>(a, g);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -513,7 +547,7 @@ bool qmvs_supported(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
     // number of groups per row keeps the scale rows 4-byte aligned for the
     // 16-byte direct-to-LDS loads
     const int ks = slices(K, bits);
-    return M == 1 && ks >= 1 && ks <= 15 && (K / group_size) % 2 == 0;
+    return M >= 1 && M <= 2 && ks >= 1 && ks <= 15 && (K / group_size) % 2 == 0;
 }
 
 void qmvs_config(const QmmArgs& a, int* rows_per_blk, int* slices_out, int* blocks) {

@@ -62,7 +62,7 @@ def _qmm(lib, **kw):
     (dict(sd=2), 2, "scales/biases dtype"),
     (dict(yd=7), 1, "y dtype"),
     (dict(route=9), 1, "route"),
-    (dict(route=5, M=2), 2, "qmvs takes one row"),
+    (dict(route=5, M=3), 2, "qmvs takes one or two rows"),
     (dict(route=5, K=32768, g=64), 2, "15 KiB"),
     (dict(route=5, K=192, g=64), 2, "even K/group_size"),
     (dict(route=5, s=ctypes.c_void_p(18)), 2, "4-byte aligned"),
@@ -228,12 +228,16 @@ def test_query_route(lib):
     # 2 <= M <= 4: the LDS-staged MFMA GEMV (m tile, k-splits, codes per stage)
     route, tiles = miqmm.query_route(2, 151936, 896, 64, 4)
     assert route == miqmm.ROUTE_QMVX and tiles[0] == 2
-    for M, mt in ((2, 2), (3, 4), (4, 4)):
+    for M, mt in ((3, 4), (4, 4)):
         route, tiles = miqmm.query_route(M, 4096, 4096, 64, 4)
         assert route == miqmm.ROUTE_QMVX and tiles[0] == mt and tiles[1] in (1, 2, 4)
-    # ... except M = 3 and 4 with long outputs, and rows it does not take
-    # (min(M, 4) K > 32768): the group-diagonal MFMA GEMV
-    assert miqmm.query_route(2, 14336, 4096, 64, 4)[0] == miqmm.ROUTE_QMVX
+    # ... M = 2 on rows of 2048 codes or more: the K-sliced GEMV with both rows
+    # of x per row of codes
+    for N, K in ((14336, 4096), (4096, 14336), (4096, 4096), (6144, 4096)):
+        assert miqmm.query_route(2, N, K, 64, 4)[0] == miqmm.ROUTE_QMVS, (N, K)
+    assert miqmm.query_route(2, 4864, 896, 64, 4)[0] == miqmm.ROUTE_QMVX
+    # ... and M = 3 and 4 with long outputs, and rows the LDS-staged GEMV does
+    # not take (min(M, 4) K > 32768): the group-diagonal MFMA GEMV
     for M, N, K in ((3, 14336, 4096), (4, 14336, 4096), (3, 4096, 14336), (4, 4096, 14336)):
         assert miqmm.query_route(M, N, K, 64, 4)[0] == miqmm.ROUTE_QMV, (M, N, K)
     # qmvx needs an even number of groups per row: K = 96, g = 32 falls back to v_dot2
