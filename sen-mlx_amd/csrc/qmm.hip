@@ -27,11 +27,15 @@
 //
 // LDS layout of a tile [R rows, 64 k] (bf16): four k-slices of 16, each
 // [R rows x 32 B]; within a slice row r holds its two 16-byte halves (k 0-7,
-// 8-15) swapped when bit 3 of r is set.  gfx950's LDS serves sixteen 16-byte
-// lanes per pass (64 banks): a fragment read of 16 consecutive rows covers all
-// 64 banks once, and every fragment address is one per-lane base plus
-// compile-time offsets (slice * R * 32 + tile row * 32), which keeps address
-// registers out of the way of the 256 accumulators.
+// 8-15) swapped when bit 3 of r is set, and in the W tile swapped once more in
+// slices 2 and 3.  gfx950's LDS serves sixteen 16-byte lanes per pass (64
+// banks): a fragment read of 16 consecutive rows covers all 64 banks once, and
+// every fragment address is one of two per-lane bases plus compile-time
+// offsets (slice * R * 32 + tile row * 32), which keeps address registers out
+// of the way of the 256 accumulators.  The extra swap is for the W stores: the
+// two lanes of a row write slices s and s + 2 (R * 64 bytes apart, the same
+// banks); with it they write different halves, so a store's sixteen lanes per
+// pass cover the 64 banks once.
 //
 // Rounding the dequantized weight to bf16 before the MFMA follows MLX's qmm,
 // which dequantizes W tiles into threadgroup memory in the activation type.
@@ -98,9 +102,9 @@ constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 
         asm volatile("" ::: "memory");            \
     } while (0)
 
-// byte offset of the 16-byte piece (k-slice kk, half fk) of row r in a tile of R rows
+// byte offset of the 16-byte piece (k-slice kk, half fk) of row r in a W tile of R rows
 __device__ __forceinline__ uint32_t lds_off(int R, int r, int kk, int fk) {
-    return kk * R * 32 + r * 32 + ((fk ^ ((r >> 3) & 1)) << 4);
+    return kk * R * 32 + r * 32 + ((fk ^ ((r >> 3) & 1) ^ ((kk >> 1) & 1)) << 4);
 }
 
 template <int BITS, int W_PER>
@@ -340,9 +344,10 @@ __global__ __launch_bounds__((64 * waves_per_block<BITS, BN>()), 1) void qmm_ker
     const int frow = lane & 31, fk = lane >> 5;
     // per-lane part of a fragment address: row frow of a 32-row tile, half fk
     const uint32_t fbase = (uint32_t)frow * 32 + ((fk ^ ((frow >> 3) & 1)) << 4);
+    const uint32_t fbase_w2 = fbase ^ 16u;  // W tile, k-slices 2 and 3
     auto read_frags = [&](int kt, int kk, bf16x8_t* af, bf16x8_t* bf) {
         const char* sA = smem + (kt % XST) * A_STAGE + fbase;
-        const char* sB = smem + B_BASE + (kt & 1) * B_STAGE + fbase;
+        const char* sB = smem + B_BASE + (kt & 1) * B_STAGE + ((kk & 2) ? fbase_w2 : fbase);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
             af[i] = *reinterpret_cast<const bf16x8_t*>(sA + kk * kBM * 32 + (wm * WM + i * 32) * 32);
