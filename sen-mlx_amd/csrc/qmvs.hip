@@ -281,11 +281,13 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     const bool t_mine = one ? (lane & (64 / RV - 1)) == 0 && t_row < nrows : ws == 0 && t_v < RV && t_row < nrows;
     const int t_glob = r0 + t_row;
     const int t_p = (t_glob >= grp.row0[0]) + (t_glob >= grp.row0[1]) + (t_glob >= grp.row0[2]);
-    const size_t t_off = ((size_t)t_m * P.N + (size_t)(t_glob - (t_p == 0 ? 0 : grp.row0[t_p - 1]))) * ysz;
+    const size_t t_n = (size_t)(t_glob - (t_p == 0 ? 0 : grp.row0[t_p - 1]));  // output column in its problem
+    const size_t t_off = ((size_t)t_m * P.N + t_n) * ysz;
     uint32_t bias_bits = 0;
     if constexpr (BIAS) {  // every lane loads (a lane past the rows reads row 0's): one load, counted below
+        // the bias is per output column, the same for every row of x
         const char* const bp0 = t_p == 0 ? (const char*)P.bias : (const char*)grp.bias[t_p - 1];
-        const char* const ba = t_mine ? bp0 + t_off : (const char*)P.bias;
+        const char* const ba = t_mine ? bp0 + t_n * ysz : (const char*)P.bias;
         if constexpr (YF32) bias_bits = *reinterpret_cast<const uint32_t*>(ba);
         else bias_bits = *reinterpret_cast<const uint16_t*>(ba);
     }
