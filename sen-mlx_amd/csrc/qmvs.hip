@@ -28,12 +28,13 @@
 // The arithmetic per chunk is the exact factorised dequant of the other
 // GEMVs: sum_k x_k (s q_k + b) = s * sum_k x_k q_k + b * sum_k x_k, with the
 // codes made exact 16-bit float operands by one and-or with a magic
-// exponent: 4-bit codes as fp16 1024 + q (bits 0-3) or 1024 + 16 q (bits
-// 4-7), one shift per word of eight codes, against x scaled per lane by an
-// exact power of two (and by 1/16 for the second kind) into fp16; 8-bit
-// codes as the bf16 top half of their fp32 value against bf16 x.  The
-// offsets and scales are undone per row in fp32:
-//   sum_k x_k q_k = 2^E (dot - 1024 * sum of the x operands).
+// exponent: 4-bit codes as bf16 128 + q against x re-paired to match, or
+// (one row of x, 16 full rows per lane: f16_operands) as fp16 1024 + q
+// (bits 0-3) or 1024 + 16 q (bits 4-7), one shift per word of eight codes,
+// against x scaled per lane by an exact power of two (and by 1/16 for the
+// second kind) into fp16; 8-bit codes as the bf16 top half of their fp32
+// value against bf16 x.  The offsets and scales are undone per row in fp32:
+//   sum_k x_k q_k = dot - 128 * sum x, or 2^E (dot - 1024 * sum of the x operands).
 // Measured on MI355X (cold weights, back-to-back graph launches, 4-bit g64):
 // M = 1, 4096 -> 14336 and 14336 -> 4096 in 7.9 us (4.2 TB/s) against 9.2 and
 // 9.9 us for the v_dot2 GEMV; the 5376 -> 262144 head in 113 us (7.0 TB/s);
@@ -50,11 +51,18 @@ namespace {
 constexpr int kSliceBytes = 1024;  // codes per K-slice: 64 lanes x 16 bytes
 
 
-// fp16 operands for the 4-bit unpack (codes at bits 0-3 and 4-7 of each
-// half are exact fp16 mantissas, one shift per word fewer than bf16)
-#ifndef QMVS_F16
-#define QMVS_F16 1
-#endif
+// Operands of the 4-bit dot products: fp16 (codes at bits 0-3 and 4-7 of each
+// half are exact fp16 mantissas: per word of eight codes one shift and four
+// and-ors, against three shifts and four for bf16) costs x a preparation of
+// ~180 VALU instructions per lane (its largest exponent, a power-of-two scale
+// and the conversions) against ~30 for bf16 (a re-pairing), so it pays only
+// where a lane has many rows to amortise it: one row of x and 16 full rows per
+// lane (measured on MI355X, 4-bit g64: 14336 -> 4096 8.39 -> 8.13 us with fp16;
+// with bf16 the decode step's launches 2.47 -> 2.36 us (q/k/v), 3.33 -> 3.13
+// (gate/up), 896 -> 4864 2.95 -> 2.71 us, and two rows of x, 4096 -> 14336,
+// 10.8 -> 9.8 us)
+template <int BITS, int RB, bool HALF, int MX>
+constexpr bool f16_operands() { return BITS == 4 && MX == 1 && RB == 16 && !HALF; }
 typedef __attribute__((ext_vector_type(2))) _Float16 half2_t;
 
 
@@ -280,6 +288,7 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     const int t_row = HALF ? (t_v / (RV / 2)) * (RB / 2) + t_v % (RB / 2) : t_v % RB;
     const bool t_mine = one ? (lane & (64 / RV - 1)) == 0 && t_row < nrows : ws == 0 && t_v < RV && t_row < nrows;
     const int t_glob = r0 + t_row;
+    constexpr bool F16 = f16_operands<BITS, RB, HALF, MX>();
     const int t_p = (t_glob >= grp.row0[0]) + (t_glob >= grp.row0[1]) + (t_glob >= grp.row0[2]);
     const size_t t_n = (size_t)(t_glob - (t_p == 0 ? 0 : grp.row0[t_p - 1]));  // output column in its problem
     const size_t t_off = ((size_t)t_m * P.N + t_n) * ysz;
@@ -296,21 +305,18 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     // x prepared: pairs (x_j, x_{j+4}) matching the 4-bit unpack, and the sum
     uint32_t X[MX][NP];
     float xs[MX];
-#if QMVS_F16
-    float xsc[MX], xoff[MX];
-#endif
+    float xsc[MX], xoff[MX];  // fp16 operands only
 #pragma unroll
     for (int m = 0; m < MX; ++m) {
         xs[m] = 0.f;
 #pragma unroll
         for (int i = 0; i < NP; ++i) xs[m] = dot2(xw[m][i], kOnesBf16x2, xs[m]);
-#if QMVS_F16
         // fp16 operands: x scaled by 2^-E (E: exponent of the chunk's largest
         // |x|, so every operand is below 2 and exact unless below fp16's normal
         // range), the operands facing the codes taken at bits 4-7 further by
         // 1/16; xsc = 2^E and xoff = -2^E * 1024 * (sum of the operands) undo
         // the scale and the codes' 1024 offset
-        if constexpr (BITS == 4) {
+        if constexpr (F16) {
             uint32_t emax = 0;
 #pragma unroll
             for (int i = 0; i < NP; ++i) emax = max(emax, max((xw[m][i] >> 7) & 0xFFu, (xw[m][i] >> 23) & 0xFFu));
@@ -335,9 +341,7 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
                                                   __builtin_bit_cast(half2_t, 0x3C003C00u), ssum, false);
             }
             xoff[m] = -xsc[m] * 1024.f * ssum;
-        } else
-#endif
-        if constexpr (BITS == 4) {
+        } else if constexpr (BITS == 4) {
 #pragma unroll
             for (int wi = 0; wi < 4; ++wi) perm_x_for4(&xw[m][4 * wi], &X[m][4 * wi]);
         } else {
@@ -354,9 +358,7 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     asm volatile("" ::: "memory");
 
     const uint32_t kMask = vgpr_const(0x000F000Fu), kMagic = kMagic128x2;
-#if QMVS_F16
-    const uint32_t kMaskHi = vgpr_const(0x00F000F0u);
-#endif
+    const uint32_t kMaskHi = vgpr_const(0x00F000F0u);  // fp16 operands only
     // this lane's scale / bias of row j at j * sb + 2 * (group in slice)
     const uint32_t sl_off = (uint32_t)((lc << CPC_SHIFT) >> gs_shift) * 2;
     // per-lane partial of every row; in the wave of the slice that runs past
@@ -375,8 +377,7 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
                 s = cv ? s : 0.f;
                 b = cv ? b : 0.f;
             }
-#if QMVS_F16
-            if constexpr (BITS == 4) {
+            if constexpr (F16) {
                 constexpr uint32_t kMagic1024 = 0x64006400u;  // fp16 1024 | q: exact 1024 + q (and 1024 + 16 q)
 #pragma unroll
                 for (int wi = 0; wi < 4; ++wi) {
@@ -397,7 +398,6 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
                 }
                 continue;
             }
-#endif
 #pragma unroll
             for (int wi = 0; wi < 4; ++wi) {
                 if constexpr (BITS == 4) unpack4_magic(q[j][wi], &p[wi * 4], kMask, kMagic);
