@@ -101,39 +101,28 @@ int check_launch(hipError_t e, const char* what) {
     return ok();
 }
 
-// Rows of at least this many codes take the K-sliced GEMV at M = 1 (one
-// wave per 1 KiB slice of codes); so do rows of at most 32 16-byte chunks
-// (the half-wave rows, two rows per wave slice).  Rows in between would
-// leave a quarter to half of the lanes idle and keep the v_dot2 GEMV.
-constexpr int64_t kMinSlicedK = 2048;
-bool short_rows(int64_t K, int bits) { return K * bits / 128 <= 32; }
-
-// Measured on MI355X (4-bit g64, cold weights):
-//   M = 1, K >= 2048: the K-sliced GEMV (4096 -> 14336: 7.8 us against 8.6 us);
-//   M = 1, rows of at most 32 chunks: the K-sliced GEMV on half-wave rows
-//          (896 -> 896 2.34 us against 2.51; 896 -> 9728 3.23 against 3.43;
-//          the 896 -> 151936 head 14.3 us against 17.9 for the LDS-staged
-//          MFMA GEMV and 19.3 for v_dot2);
-//   M = 1, other rows: the v_dot2 GEMV, except for many-row heads with K <=
+// Measured on MI355X (4-bit g64 unless noted, cold weights):
+//   M <= 4: the K-sliced GEMV wherever it takes the shape (rows of at most 15
+//          KiB of codes, 8 KiB with more than two rows of x; an even number of
+//          groups; 4-byte aligned scales and biases): each row of codes is
+//          unpacked once for every row of x and dotted on v_dot2.  M = 1:
+//          4096 -> 14336 8.4 us against 8.6 for v_dot2, rows of 33-63 chunks
+//          (1536 -> 4096) 2.98 against 3.75, the 896 -> 151936 head 14.3
+//          against 17.9 for the LDS-staged MFMA GEMV; M = 2: 4096 -> 14336 9.8
+//          against 12.3 (LDS-staged MFMA), 896 -> 4864 2.99 against 3.6; M = 3
+//          / 4: 4096 -> 6144 7.3 / 7.7 against 9.1 / 9.0 (LDS-staged MFMA),
+//          4096 -> 14336 12.1 / 12.5 against 13.0 / 13.1 (group-diagonal
+//          MFMA); 8-bit, M = 4, 4096 -> 14336: 15.0 against 25.7;
+//   M = 1, other shapes: the v_dot2 GEMV, except for many-row heads with K <=
 //          2048, where the LDS-staged MFMA GEMV wins;
-//   M = 2, K >= 2048: the K-sliced GEMV with both rows of x per row of codes
-//          (4096 -> 14336 10.5 us against 12.3 for the LDS-staged MFMA GEMV;
-//          4096 -> 6144 5.7 against 7.8; on rows of 896 it is slower);
-//   2 <= M <= 4: the LDS-staged MFMA GEMV (4096 -> 14336: 12.8 / 16.0 us at
-//          M = 2 / 4 against 15.1 / 22.2 us for v_dot2) when it supports the
+//   2 <= M <= 4, other shapes: the LDS-staged MFMA GEMV when it supports the
 //          shape (min(M, 4) K <= 32768), except at M = 3 and 4 with N >= 8192,
-//          where the group-diagonal MFMA GEMV is faster (4096 -> 14336, M = 4:
-//          16.1 -> 13.2 us; at 4096 x 4096 it is slower, 6.6 -> 7.3 us); rows
-//          the LDS-staged GEMV does not take go to the group-diagonal one too
-//          (14336 -> 4096, M = 4, with a workspace: 22.6 us on v_dot2 -> 13.7);
+//          where the group-diagonal MFMA GEMV is faster; rows the LDS-staged
+//          GEMV does not take go to the group-diagonal one too;
 //   5 <= M <= 16: the group-diagonal MFMA GEMV, whose cost barely grows with M;
 //   larger M: the tiled MFMA matmul.
 int auto_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, bool sb_aligned4 = true) {
-    if (M == 1 && (K >= kMinSlicedK || short_rows(K, bits)) && sb_aligned4 &&
-        miqmm::qmvs_supported(M, N, K, bits, group_size))
-        return MIQMM_ROUTE_QMVS;
-    if (M == 2 && K >= kMinSlicedK && sb_aligned4 && miqmm::qmvs_supported(M, N, K, bits, group_size))
-        return MIQMM_ROUTE_QMVS;
+    if (M <= 4 && sb_aligned4 && miqmm::qmvs_supported(M, N, K, bits, group_size)) return MIQMM_ROUTE_QMVS;
     if (M == 1) {
         const bool wide_head = N >= 65536 && K <= 2048 && miqmm::qmvx_supported(M, K, group_size);
         return wide_head ? MIQMM_ROUTE_QMVX : MIQMM_ROUTE_QMV_DOT;
@@ -160,10 +149,12 @@ int check_args(void* y, const void* x, const uint32_t* w, const void* scales, co
     if (route != MIQMM_ROUTE_AUTO && route != MIQMM_ROUTE_QMV && route != MIQMM_ROUTE_QMM &&
         route != MIQMM_ROUTE_QMV_DOT && route != MIQMM_ROUTE_QMVX && route != MIQMM_ROUTE_QMVS)
         return fail(MIQMM_EINVAL, "route %d invalid", route);
-    if (route == MIQMM_ROUTE_QMVS && M > 2)
-        return fail(MIQMM_ENOTSUP, "route qmvs takes one or two rows of x (M <= 2)");
-    if (route == MIQMM_ROUTE_QMVS && !miqmm::qmvs_supported(1, N, K, bits, group_size))
-        return fail(MIQMM_ENOTSUP, "route qmvs needs K*bits/8 <= 15 KiB and an even K/group_size");
+    if (route == MIQMM_ROUTE_QMVS && M > 4)
+        return fail(MIQMM_ENOTSUP, "route qmvs takes one to four rows of x (M <= 4)");
+    if (route == MIQMM_ROUTE_QMVS && !miqmm::qmvs_supported(M > 1 ? M : 1, N, K, bits, group_size))
+        return fail(MIQMM_ENOTSUP,
+                    "route qmvs needs K*bits/8 <= 15 KiB (8 KiB with more than two rows of x) and an even "
+                    "K/group_size");
     if (route == MIQMM_ROUTE_QMVS && M > 0 && (!aligned4(scales) || !aligned4(biases)))
         return fail(MIQMM_ENOTSUP, "route qmvs needs 4-byte aligned scales and biases");
     if (route == MIQMM_ROUTE_QMVX && !miqmm::qmvx_supported(M < 4 ? M : 4, K, group_size))
@@ -392,7 +383,7 @@ int miqmm_quantized_matmul_grouped(const miqmm_problem* problems, int count, int
     miqmm::QmmArgs a[miqmm::kMaxGroup];
     // one row of x and problems stored one after another (fused at load),
     // with rows the K-sliced GEMV takes: one launch over all their rows
-    if (M == 1 && count <= miqmm::kMaxGroup && (K >= kMinSlicedK || short_rows(K, bits)) &&
+    if (M == 1 && count <= miqmm::kMaxGroup &&
         aligned4(problems[0].scales) && aligned4(problems[0].biases)) {
         for (int i = 0; i < count; ++i) {
             const miqmm_problem& p = problems[i];

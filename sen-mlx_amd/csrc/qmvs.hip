@@ -183,25 +183,30 @@ __device__ __forceinline__ float transposed_sum(const float (&v)[RB], int lane) 
 
 // RB rows per block; ND direct-to-LDS loads per scale (and bias) array:
 // RB * (bytes of scales per row and slice) / 1 KiB, rounded up
-template <int RB>
-constexpr int max_threads() { return RB >= 32 ? 512 : 1024; }  // 32 rows of codes take 128 registers
+// waves (K-slices) per block: up to 15, or 8 where a lane needs more than 128
+// registers (32 rows of codes; four rows of x)
+template <int RB, int MX>
+constexpr int max_threads() { return RB >= 32 || MX == 4 ? 512 : 1024; }
+constexpr int max_slices(int64_t M) { return M > 2 ? 8 : 15; }
 
 // The arguments are scalars, the ones the first loads need leading: the build
 // preloads leading kernel arguments into SGPRs at wave launch, which spares
 // the scalar memory round trip before the first load (bias, read last, is
 // past the preloaded registers).  meta = log2 group size | y dtype << 8 |
-// waves per block << 16 (blockDim would be a load of the implicit arguments).
+// waves per block << 16 | rows of x << 24 (blockDim would be a load of the
+// implicit arguments).
 //
 // HALF (rows of at most 32 chunks, one slice): the wave's halves compute
 // different rows, lanes 32h .. 32h + 31 the rows h RB/2 .. h RB/2 + RB/2 - 1
 // of the block, so no lane idles past a short row's end (K = 896 at 4 bits
 // is 28 chunks); the reduction starts from its 32-lane state.
 //
-// MX rows of x (1 or 2): each row of codes is unpacked once and dotted with
+// MX rows of x (1, 2 or 4; three rows run as four, the fourth reading zeros and
+// storing nothing): each row of codes is unpacked once and dotted with
 // every row of x; the wave reduces RB * MX sums (value m * RB + j, or with
 // HALF m * RB/2 + j in each half).
 template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF, int MX>
-__global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t* xp, const uint32_t* wp,
+__global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uint16_t* xp, const uint32_t* wp,
                                                                  const uint16_t* sp, const uint16_t* bp, int n, int k,
                                                                  uint32_t meta, void* yp, const void* biasp,
                                                                  const QmvsGroup grp) {
@@ -214,7 +219,7 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int lane = threadIdx.x & 63;
     const int ws = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's K-slice
-    const int KS = (int)(meta >> 16);
+    const int KS = (int)((meta >> 16) & 0xff);
     const int K = P.K, gs_shift = P.gs_shift;
     const int C = K >> CPC_SHIFT;       // chunks per row
     constexpr int RL = HALF ? RB / 2 : RB;          // rows per lane
@@ -229,11 +234,12 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     constexpr int ysz = YF32 ? 4 : 2;
 
     constexpr int RV = RB * MX;  // sums the wave reduces
-    // x chunk of this lane in each row of x (zero past the row end); prepared
-    // below, once the codes are in flight
+    const int MR = (int)(meta >> 24);  // rows of x (MX, or 3 with MX = 4)
+    // x chunk of this lane in each row of x (zero past the row end and past
+    // the last row); prepared below, once the codes are in flight
     uint32_t xw[MX][NP];
     {
-        const auto xr = make_rsrc(P.x, (uint32_t)(MX * K) * 2);
+        const auto xr = make_rsrc(P.x, (uint32_t)(MR * K) * 2);
 #pragma unroll
         for (int m = 0; m < MX; ++m)
 #pragma unroll
@@ -286,7 +292,7 @@ __global__ __launch_bounds__(max_threads<RB>()) void qmvs_kernel(const uint16_t*
     const int t_v = one ? lane / (64 / RV) : lane;
     const int t_m = HALF ? (t_v % (RV / 2)) / (RB / 2) : t_v / RB;
     const int t_row = HALF ? (t_v / (RV / 2)) * (RB / 2) + t_v % (RB / 2) : t_v % RB;
-    const bool t_mine = one ? (lane & (64 / RV - 1)) == 0 && t_row < nrows : ws == 0 && t_v < RV && t_row < nrows;
+    const bool t_mine = (one ? (lane & (64 / RV - 1)) == 0 : ws == 0 && t_v < RV) && t_row < nrows && t_m < MR;
     const int t_glob = r0 + t_row;
     constexpr bool F16 = f16_operands<BITS, RB, HALF, MX>();
     const int t_p = (t_glob >= grp.row0[0]) + (t_glob >= grp.row0[1]) + (t_glob >= grp.row0[2]);
@@ -483,7 +489,8 @@ hipError_t launch_t(const QmmArgs& a, const QmvsGroup& g, int ks) {
     const size_t lds = (size_t)ks * wave_lds<ND>() + (size_t)ks * RB * MX * 4;
     const int blocks = (int)((a.N + RB - 1) / RB);
     hipLaunchKernelGGL((qmvs_kernel<BITS, SBT, RB, ND, YF32, BIAS, HALF, MX>), dim3(blocks), dim3(64 * ks), lds, a.stream, P.x,
-                       P.w, P.s, P.b, P.N, P.K, (uint32_t)P.gs_shift | (uint32_t)P.y_dtype << 8 | (uint32_t)ks << 16, P.y,
+                       P.w, P.s, P.b, P.N, P.K,
+                       (uint32_t)P.gs_shift | (uint32_t)P.y_dtype << 8 | (uint32_t)ks << 16 | (uint32_t)a.M << 24, P.y,
                        P.bias, g);
     return hipGetLastError();
 }
@@ -509,11 +516,15 @@ hipError_t launch_nd(const QmmArgs& a, const QmvsGroup& g, int ks) {
 template <int BITS, int SBT, bool YF32, bool BIAS, int MX>
 hipError_t launch_rb(const QmmArgs& a, const QmvsGroup& g) {
     const int ks = slices(a.K, BITS);
-    switch (rows_per_block(a.N, ks)) {
+    int rb = rows_per_block(a.N, ks);
+    if (MX == 4 && rb > 8) rb = 8;  // RB * MX <= 32 sums per wave
+    switch (rb) {
 #if QMVS_RB_FORCE == 32
         case 32: return launch_nd<BITS, SBT, 32, YF32, BIAS, 1>(a, g, ks);
 #endif
-        case 16: return launch_nd<BITS, SBT, 16, YF32, BIAS, MX>(a, g, ks);
+        case 16:
+            if constexpr (MX < 4) return launch_nd<BITS, SBT, 16, YF32, BIAS, MX>(a, g, ks);
+            [[fallthrough]];
         case 8: return launch_nd<BITS, SBT, 8, YF32, BIAS, MX>(a, g, ks);
         default: return launch_nd<BITS, SBT, 4, YF32, BIAS, MX>(a, g, ks);
     }
@@ -534,10 +545,12 @@ hipError_t launch_m(const QmmArgs& a, const QmvsGroup& g) {
     return a.bias ? launch_y<false, true, MX>(a, g) : launch_y<false, false, MX>(a, g);
 }
 
-// one or two rows of x (two: no grouped problems)
+// one to four rows of x (more than one: no grouped problems)
 hipError_t launch_g(const QmmArgs& a, const QmvsGroup& g) {
     if (a.M == 1) return launch_m<1>(a, g);
-    if (a.M == 2 && g.row0[0] == INT_MAX) return launch_m<2>(a, g);
+    if (g.row0[0] != INT_MAX) return hipErrorInvalidValue;
+    if (a.M == 2) return launch_m<2>(a, g);
+    if (a.M == 3 || a.M == 4) return launch_m<4>(a, g);
     return hipErrorInvalidValue;
 }
 
@@ -545,11 +558,12 @@ hipError_t launch_g(const QmmArgs& a, const QmvsGroup& g) {
 
 bool qmvs_supported(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
     (void)N;
-    // up to 15 waves per block (LDS within the default 64 KiB); an even
+    // up to 15 waves per block, 8 with more than two rows of x (LDS within
+    // the default 64 KiB; the registers of four rows of x); an even
     // number of groups per row keeps the scale rows 4-byte aligned for the
     // 16-byte direct-to-LDS loads
     const int ks = slices(K, bits);
-    return M >= 1 && M <= 2 && ks >= 1 && ks <= 15 && (K / group_size) % 2 == 0;
+    return M >= 1 && M <= 4 && ks >= 1 && ks <= max_slices(M) && (K / group_size) % 2 == 0;
 }
 
 void qmvs_config(const QmmArgs& a, int* rows_per_blk, int* slices_out, int* blocks) {

@@ -62,7 +62,7 @@ def _qmm(lib, **kw):
     (dict(sd=2), 2, "scales/biases dtype"),
     (dict(yd=7), 1, "y dtype"),
     (dict(route=9), 1, "route"),
-    (dict(route=5, M=3), 2, "qmvs takes one or two rows"),
+    (dict(route=5, M=5), 2, "qmvs takes one to four rows"),
     (dict(route=5, K=32768, g=64), 2, "15 KiB"),
     (dict(route=5, K=192, g=64), 2, "even K/group_size"),
     (dict(route=5, s=ctypes.c_void_p(18)), 2, "4-byte aligned"),
@@ -222,23 +222,20 @@ def test_query_route(lib):
     # rows per wave slice; 4 rows per block below ~3 waves per CU
     assert miqmm.query_route(1, 4864, 896, 64, 4) == (miqmm.ROUTE_QMVS, (4, 1, 1216, 0))
     assert miqmm.query_route(1, 151936, 896, 64, 4) == (miqmm.ROUTE_QMVS, (16, 1, 9496, 0))
-    # rows in between: the v_dot2 GEMV, lanes per row by chunk count
-    route, tiles = miqmm.query_route(1, 4864, 1536, 64, 4)
-    assert route == miqmm.ROUTE_QMV_DOT and tiles[2] == 16  # 48 chunks per row -> 16 lanes, no idle one
-    # 2 <= M <= 4: the LDS-staged MFMA GEMV (m tile, k-splits, codes per stage)
-    route, tiles = miqmm.query_route(2, 151936, 896, 64, 4)
+    # and rows in between (48 chunks: one slice, a quarter of the lanes idle)
+    assert miqmm.query_route(1, 4864, 1536, 64, 4) == (miqmm.ROUTE_QMVS, (4, 1, 1216, 0))
+    # 2 <= M <= 4: the K-sliced GEMV too, each row of codes unpacked once for
+    # every row of x (three rows as four), on rows of up to 15 KiB of codes
+    # (8 KiB with more than two rows of x)
+    for M in (2, 3, 4):
+        for N, K in ((14336, 4096), (4096, 14336), (4096, 4096), (6144, 4096), (4864, 896), (151936, 896)):
+            assert miqmm.query_route(M, N, K, 64, 4)[0] == miqmm.ROUTE_QMVS, (M, N, K)
+    # longer rows: the LDS-staged MFMA GEMV where it takes them (x of the
+    # padded M rows within 64 KiB) ...
+    route, tiles = miqmm.query_route(2, 4096, 16384, 64, 8)  # 16 KiB of codes per row
     assert route == miqmm.ROUTE_QMVX and tiles[0] == 2
-    for M, mt in ((3, 4), (4, 4)):
-        route, tiles = miqmm.query_route(M, 4096, 4096, 64, 4)
-        assert route == miqmm.ROUTE_QMVX and tiles[0] == mt and tiles[1] in (1, 2, 4)
-    # ... M = 2 on rows of 2048 codes or more: the K-sliced GEMV with both rows
-    # of x per row of codes
-    for N, K in ((14336, 4096), (4096, 14336), (4096, 4096), (6144, 4096)):
-        assert miqmm.query_route(2, N, K, 64, 4)[0] == miqmm.ROUTE_QMVS, (N, K)
-    assert miqmm.query_route(2, 4864, 896, 64, 4)[0] == miqmm.ROUTE_QMVX
-    # ... and M = 3 and 4 with long outputs, and rows the LDS-staged GEMV does
-    # not take (min(M, 4) K > 32768): the group-diagonal MFMA GEMV
-    for M, N, K in ((3, 14336, 4096), (4, 14336, 4096), (3, 4096, 14336), (4, 4096, 14336)):
+    # ... else the group-diagonal MFMA GEMV
+    for M, N, K in ((3, 4096, 20480), (4, 4096, 20480)):
         assert miqmm.query_route(M, N, K, 64, 4)[0] == miqmm.ROUTE_QMV, (M, N, K)
     # qmvx needs an even number of groups per row: K = 96, g = 32 falls back to v_dot2
     assert miqmm.query_route(2, 128, 96, 32, 4)[0] == miqmm.ROUTE_QMV_DOT
@@ -263,10 +260,11 @@ def test_query_route(lib):
     assert miqmm.query_route(16, 4096, 14336, 64, 4)[1] == (1, 16, 4, 0)
     # with a workspace the MFMA GEMV splits K where long rows or a long
     # output at M > 8 make that faster: S k ranges of fp32 partials
-    for M, N, K in ((16, 4096, 14336), (8, 4096, 14336), (16, 14336, 4096), (5, 512, 8192), (4, 4096, 14336)):
+    for M, N, K in ((16, 4096, 14336), (8, 4096, 14336), (16, 14336, 4096), (5, 512, 8192), (4, 4096, 20480)):
         n = miqmm.workspace_size(M, N, K)
         assert n > 0 and n % (M * N * 4) == 0 and n // (M * N * 4) <= 16, (M, N, K, n)
-    for M, N, K in ((8, 14336, 4096), (16, 4096, 4096), (1, 4096, 14336), (2, 4096, 14336), (4, 14336, 4096)):
+    for M, N, K in ((8, 14336, 4096), (16, 4096, 4096), (1, 4096, 14336), (2, 4096, 14336), (4, 14336, 4096),
+                    (4, 4096, 14336)):
         assert miqmm.workspace_size(M, N, K) == 0, (M, N, K)
     with pytest.raises(miqmm.MiqmmError) as e:
         miqmm.query_route(1, 64, 96, 64, 4)
