@@ -51,11 +51,12 @@ typedef enum { MIQMM_DT_BF16 = 0, MIQMM_DT_F16 = 1, MIQMM_DT_F32 = 2 } miqmm_dty
 /* QMV: small-M GEMV on MFMA with exact integer codes; QMM: large-M tiled MFMA
  * with bf16-dequantized W tiles; QMV_DOT: small-M GEMV on v_dot2 (no MFMA);
  * QMVX: small-M GEMV on MFMA with x staged in LDS (M <= 4 per pass, needs
- * K/group_size even and min(M,4)*K <= 32768); QMVS: one- or two-row GEMV on
- * v_dot2 with K cut into 1 KiB slices of codes, one wave per slice, or two
- * rows of W per wave on rows of at most 32 chunks (M <= 2, needs
- * K*bits/8 <= 15 KiB, K/group_size even, scales and biases 4-byte aligned;
- * with M == 2 each wave dots its unpacked codes with both rows of x). */
+ * K/group_size even and min(M,4)*K <= 32768); QMVS: GEMV on v_dot2 for one to
+ * four rows of x with K cut into 1 KiB slices of codes, one wave per slice, or
+ * two rows of W per wave on rows of at most 32 chunks (M <= 4, needs
+ * K*bits/8 <= 15 KiB -- 8 KiB with M > 2 --, K/group_size even, scales and
+ * biases 4-byte aligned; each wave dots its unpacked codes with every row of
+ * x). */
 typedef enum {
     MIQMM_ROUTE_AUTO = 0,
     MIQMM_ROUTE_QMV = 1,
@@ -71,13 +72,12 @@ typedef enum {
  * (reached at src/engine/mlx_lm/utils/mod.rs:70-78 and from every
  * QuantizedLinear::forward).  transpose must be 1; bits in {4, 8};
  * group_size in {32, 64, 128}; K % group_size == 0; x and w 16-byte aligned.
- * M == 0 is a no-op.  Route (HBM-bound GEMVs for M <= 16): M == 1 -> qmvs
- * for K >= 2048 or rows of at most 32 16-byte chunks (K <= 1024 at 4 bits,
- * 512 at 8; two rows per wave slice), with K*bits/8 <= 15 KiB, K/group_size
- * even and 4-byte aligned scales and biases; else qmv_dot, or qmvx for
- * N >= 65536 with K <= 2048; M == 2 -> qmvs for K >= 2048 under the same
- * conditions; 2 <= M <= 4 -> qmvx where supported, else qmv_dot; M <= 16 ->
- * qmv; else qmm (MFMA-bound tiled matmul).
+ * M == 0 is a no-op.  Route (HBM-bound GEMVs for M <= 16): M <= 4 -> qmvs
+ * wherever it takes the shape (K*bits/8 <= 15 KiB, 8 KiB with M > 2;
+ * K/group_size even; 4-byte aligned scales and biases); else M == 1 ->
+ * qmv_dot, or qmvx for N >= 65536 with K <= 2048; 2 <= M <= 4 -> qmvx where
+ * supported, else qmv (or qmv_dot with an odd K/group_size); M <= 16 -> qmv;
+ * else qmm (MFMA-bound tiled matmul).
  */
 int miqmm_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
                            const void* biases, int64_t M, int64_t N, int64_t K, int transpose,
