@@ -76,14 +76,28 @@ struct QmvsArgs {
     int N, K, gs_shift, y_dtype;
 };
 
-// Problems 1..3 of a contiguous group: their codes, scales and biases
-// follow problem 0's (the kernel reads one matrix of all their rows); row0
-// is each one's first row in it (unused: INT_MAX) and y / bias its output
-// and bias.  Problem 0's are the kernel's own y and bias.
+// Problems 1..3 of a group (one row of x shared by all); problem 0 is the
+// kernel's own arguments.  Contiguous (codes, scales and biases following
+// problem 0's): the kernel reads one matrix of all their rows, and row0 is
+// each one's first row in it (unused: INT_MAX), y / bias its output and
+// bias.  Separate (the NC kernels): w / s / b are its own codes, scales and
+// biases, n its rows and blk0 its first block; every block computes rows of
+// one problem and every problem starts a block.  With the rows per block of
+// the problems' concatenation either way gives each row bit for bit as a
+// launch over that one matrix: a row's sum does not depend on where in a
+// block it sits.  (The separate layout's per-block lookup reads arguments
+// past the preloaded ones before the first loads, a scalar memory round trip
+// the other launches do not take.)
 struct QmvsGroup {
     void* y[3];
     const void* bias[3];
     int row0[3];
+    const uint32_t* w[3];
+    const uint16_t* s[3];
+    const uint16_t* b[3];
+    int n[3];
+    int blk0[3];
+    int n_first;  // NC: rows of problem 0 (0: not a separate-allocation group)
 };
 
 // LDS per wave: scales then biases of its rows, ND KiB each (a direct-to-LDS
@@ -205,7 +219,7 @@ constexpr int max_slices(int64_t M) { return M > 2 ? 8 : 15; }
 // storing nothing): each row of codes is unpacked once and dotted with
 // every row of x; the wave reduces RB * MX sums (value m * RB + j, or with
 // HALF m * RB/2 + j in each half).
-template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF, int MX>
+template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF, int MX, bool NC>
 __global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uint16_t* xp, const uint32_t* wp,
                                                                  const uint16_t* sp, const uint16_t* bp, int n, int k,
                                                                  uint32_t meta, void* yp, const void* biasp,
@@ -229,8 +243,16 @@ __global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uin
     const bool cv = c < C;
     const uint32_t row_bytes = (uint32_t)K * BITS / 8;
     const int G = K >> gs_shift;
-    const int r0 = blockIdx.x * RB;
-    const int nrows = min(RB, P.N - r0);
+    // NC: this block's problem (uniform) and its first row in it
+    const int bx = blockIdx.x;
+    const int gp = NC ? (bx >= grp.blk0[0]) + (bx >= grp.blk0[1]) + (bx >= grp.blk0[2]) : 0;
+    const int r0 = NC ? (bx - (gp == 0 ? 0 : gp == 1 ? grp.blk0[0] : gp == 2 ? grp.blk0[1] : grp.blk0[2])) * RB
+                      : bx * RB;
+    const int Np = !NC || gp == 0 ? P.N : gp == 1 ? grp.n[0] : gp == 2 ? grp.n[1] : grp.n[2];
+    const uint32_t* const pw = !NC || gp == 0 ? P.w : gp == 1 ? grp.w[0] : gp == 2 ? grp.w[1] : grp.w[2];
+    const uint16_t* const ps = !NC || gp == 0 ? P.s : gp == 1 ? grp.s[0] : gp == 2 ? grp.s[1] : grp.s[2];
+    const uint16_t* const pb = !NC || gp == 0 ? P.b : gp == 1 ? grp.b[0] : gp == 2 ? grp.b[1] : grp.b[2];
+    const int nrows = min(RB, Np - r0);
     constexpr int ysz = YF32 ? 4 : 2;
 
     constexpr int RV = RB * MX;  // sums the wave reduces
@@ -262,8 +284,8 @@ __global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uin
     // scales and biases of this wave's slice of the block's rows, to LDS:
     // row j's gps scales at j * sb (sb = 2 * gps bytes, a multiple of 16);
     // DMA lane l of load d carries 16 bytes of row (d * 64 + l) / lpr
-    const auto sr = make_rsrc(P.s + (size_t)r0 * G, (uint32_t)nrows * G * 2);
-    const auto br = make_rsrc(P.b + (size_t)r0 * G, (uint32_t)nrows * G * 2);
+    const auto sr = make_rsrc(ps + (size_t)r0 * G, (uint32_t)nrows * G * 2);
+    const auto br = make_rsrc(pb + (size_t)r0 * G, (uint32_t)nrows * G * 2);
     const int gps = (kSliceBytes * 8 / BITS) >> gs_shift;
     const int sb = 2 * gps;
     const int lpr_shift = __builtin_ctz((unsigned)sb >> 4);  // DMA lanes per row: a power of two
@@ -278,7 +300,7 @@ __global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uin
     }
     __builtin_amdgcn_sched_barrier(0);
     // codes of the block's rows (rows past the block's last read zero)
-    const auto wr = make_rsrc((const char*)P.w + (size_t)r0 * row_bytes, (uint32_t)nrows * row_bytes);
+    const auto wr = make_rsrc((const char*)pw + (size_t)r0 * row_bytes, (uint32_t)nrows * row_bytes);
     u32x4_t q[RL];
 #pragma unroll
     for (int j = 0; j < RL; ++j)
@@ -295,9 +317,10 @@ __global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uin
     const bool t_mine = (one ? (lane & (64 / RV - 1)) == 0 : ws == 0 && t_v < RV) && t_row < nrows && t_m < MR;
     const int t_glob = r0 + t_row;
     constexpr bool F16 = f16_operands<BITS, RB, HALF, MX>();
-    const int t_p = (t_glob >= grp.row0[0]) + (t_glob >= grp.row0[1]) + (t_glob >= grp.row0[2]);
-    const size_t t_n = (size_t)(t_glob - (t_p == 0 ? 0 : grp.row0[t_p - 1]));  // output column in its problem
-    const size_t t_off = ((size_t)t_m * P.N + t_n) * ysz;
+    // the problem of the stored row, and its output column there
+    const int t_p = NC ? gp : (t_glob >= grp.row0[0]) + (t_glob >= grp.row0[1]) + (t_glob >= grp.row0[2]);
+    const size_t t_n = (size_t)(t_glob - (NC || t_p == 0 ? 0 : grp.row0[t_p - 1]));
+    const size_t t_off = ((size_t)t_m * Np + t_n) * ysz;
     uint32_t bias_bits = 0;
     if constexpr (BIAS) {  // every lane loads (a lane past the rows reads row 0's): one load, counted below
         // the bias is per output column, the same for every row of x
@@ -482,13 +505,23 @@ int rows_per_block(int64_t N, int ks) {
     return 4;
 }
 
-template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF, int MX>
-hipError_t launch_t(const QmmArgs& a, const QmvsGroup& g, int ks) {
+// NC: a group in separate allocations; a.N is then all the problems' rows
+// (for the rows per block of their concatenation) and n_first problem 0's
+template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF, int MX, bool NC>
+hipError_t launch_t(const QmmArgs& a, const QmvsGroup& g0, int ks, int n_first) {
+    const int n0 = NC ? n_first : (int)a.N;
     const QmvsArgs P{(const uint16_t*)a.x, a.w, (const uint16_t*)a.scales, (const uint16_t*)a.biases, a.y, a.bias,
-                     (int)a.N, (int)a.K, __builtin_ctz((unsigned)a.group_size), a.y_dtype};
+                     n0, (int)a.K, __builtin_ctz((unsigned)a.group_size), a.y_dtype};
     const size_t lds = (size_t)ks * wave_lds<ND>() + (size_t)ks * RB * MX * 4;
-    const int blocks = (int)((a.N + RB - 1) / RB);
-    hipLaunchKernelGGL((qmvs_kernel<BITS, SBT, RB, ND, YF32, BIAS, HALF, MX>), dim3(blocks), dim3(64 * ks), lds, a.stream, P.x,
+    QmvsGroup g = g0;
+    int blocks = (n0 + RB - 1) / RB;
+    if (NC) {  // each problem starts a block
+        for (int i = 0; i < 3; ++i) {
+            g.blk0[i] = g.n[i] > 0 ? blocks : INT_MAX;
+            blocks += (g.n[i] + RB - 1) / RB;
+        }
+    }
+    hipLaunchKernelGGL((qmvs_kernel<BITS, SBT, RB, ND, YF32, BIAS, HALF, MX, NC>), dim3(blocks), dim3(64 * ks), lds, a.stream, P.x,
                        P.w, P.s, P.b, P.N, P.K,
                        (uint32_t)P.gs_shift | (uint32_t)P.y_dtype << 8 | (uint32_t)ks << 16 | (uint32_t)a.M << 24, P.y,
                        P.bias, g);
@@ -500,8 +533,14 @@ bool half_rows(int64_t K, int bits) { return slices(K, bits) == 1 && K * bits / 
 
 template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, int MX>
 hipError_t launch_h(const QmmArgs& a, const QmvsGroup& g, int ks) {
-    return half_rows(a.K, BITS) ? launch_t<BITS, SBT, RB, ND, YF32, BIAS, true, MX>(a, g, ks)
-                                : launch_t<BITS, SBT, RB, ND, YF32, BIAS, false, MX>(a, g, ks);
+    const bool half = half_rows(a.K, BITS);
+    if constexpr (MX == 1) {
+        if (g.n_first > 0)
+            return half ? launch_t<BITS, SBT, RB, ND, YF32, BIAS, true, MX, true>(a, g, ks, g.n_first)
+                        : launch_t<BITS, SBT, RB, ND, YF32, BIAS, false, MX, true>(a, g, ks, g.n_first);
+    }
+    return half ? launch_t<BITS, SBT, RB, ND, YF32, BIAS, true, MX, false>(a, g, ks, 0)
+                : launch_t<BITS, SBT, RB, ND, YF32, BIAS, false, MX, false>(a, g, ks, 0);
 }
 
 template <int BITS, int SBT, int RB, bool YF32, bool BIAS, int MX>
@@ -548,7 +587,7 @@ hipError_t launch_m(const QmmArgs& a, const QmvsGroup& g) {
 // one to four rows of x (more than one: no grouped problems)
 hipError_t launch_g(const QmmArgs& a, const QmvsGroup& g) {
     if (a.M == 1) return launch_m<1>(a, g);
-    if (g.row0[0] != INT_MAX) return hipErrorInvalidValue;
+    if (g.row0[0] != INT_MAX || g.n_first > 0) return hipErrorInvalidValue;
     if (a.M == 2) return launch_m<2>(a, g);
     if (a.M == 3 || a.M == 4) return launch_m<4>(a, g);
     return hipErrorInvalidValue;
@@ -573,38 +612,62 @@ void qmvs_config(const QmmArgs& a, int* rows_per_blk, int* slices_out, int* bloc
     if (blocks) *blocks = (int)((a.N + rb - 1) / rb);
 }
 
-hipError_t launch_qmvs(const QmmArgs& a) {
-    const QmvsGroup g{{nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr}, {INT_MAX, INT_MAX, INT_MAX}};
-    return launch_g(a, g);
+namespace {
+
+QmvsGroup no_group() {
+    QmvsGroup g{};
+    for (int i = 0; i < 3; ++i) g.row0[i] = g.blk0[i] = INT_MAX;
+    return g;
 }
 
-bool qmvs_group_ok(const QmmArgs* a, int count) {
-    if (count < 2 || count > 4 || a[0].M != 1) return false;
+// a group the K-sliced GEMV takes in one launch: 1 stored one after another,
+// 2 in separate allocations, 0 neither
+int qmvs_group_kind(const QmmArgs* a, int count) {
+    if (count < 2 || count > 4 || a[0].M != 1) return 0;
     const int64_t row_bytes = a[0].K * a[0].bits / 8, sb_row = a[0].K / a[0].group_size * 2;
     int64_t rows = 0;
+    bool contiguous = true;
     for (int i = 0; i < count; ++i) {
-        if (a[i].x != a[0].x || (a[i].bias == nullptr) != (a[0].bias == nullptr)) return false;
-        if ((const char*)a[i].w != (const char*)a[0].w + rows * row_bytes) return false;
-        if ((const char*)a[i].scales != (const char*)a[0].scales + rows * sb_row) return false;
-        if ((const char*)a[i].biases != (const char*)a[0].biases + rows * sb_row) return false;
+        if (a[i].x != a[0].x || (a[i].bias == nullptr) != (a[0].bias == nullptr) || a[i].N < 1) return 0;
+        if (((reinterpret_cast<uintptr_t>(a[i].scales) | reinterpret_cast<uintptr_t>(a[i].biases)) & 3) != 0)
+            return 0;
+        contiguous = contiguous && (const char*)a[i].w == (const char*)a[0].w + rows * row_bytes &&
+                     (const char*)a[i].scales == (const char*)a[0].scales + rows * sb_row &&
+                     (const char*)a[i].biases == (const char*)a[0].biases + rows * sb_row;
         rows += a[i].N;
     }
-    return rows < ((int64_t)1 << 31) && qmvs_supported(1, rows, a[0].K, a[0].bits, a[0].group_size);
+    if (rows >= ((int64_t)1 << 31) || !qmvs_supported(1, rows, a[0].K, a[0].bits, a[0].group_size)) return 0;
+    return contiguous ? 1 : 2;
 }
 
+}  // namespace
+
+hipError_t launch_qmvs(const QmmArgs& a) { return launch_g(a, no_group()); }
+
+bool qmvs_group_ok(const QmmArgs* a, int count) { return qmvs_group_kind(a, count) != 0; }
+
 hipError_t launch_qmvs_grouped(const QmmArgs* a, int count) {
-    if (!qmvs_group_ok(a, count)) return hipErrorInvalidValue;
-    QmvsGroup g{{nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr}, {INT_MAX, INT_MAX, INT_MAX}};
-    QmmArgs all = a[0];
+    const int kind = qmvs_group_kind(a, count);
+    if (kind == 0) return hipErrorInvalidValue;
+    QmvsGroup g = no_group();
+    QmmArgs all = a[0];  // N: all the rows (the rows per block of their concatenation)
     all.N = 0;
     for (int i = 0; i < count; ++i) {
         if (i > 0) {
             g.y[i - 1] = a[i].y;
             g.bias[i - 1] = a[i].bias;
-            g.row0[i - 1] = (int)all.N;
+            if (kind == 1) {
+                g.row0[i - 1] = (int)all.N;
+            } else {
+                g.w[i - 1] = a[i].w;
+                g.s[i - 1] = static_cast<const uint16_t*>(a[i].scales);
+                g.b[i - 1] = static_cast<const uint16_t*>(a[i].biases);
+                g.n[i - 1] = (int)a[i].N;
+            }
         }
         all.N += a[i].N;
     }
+    if (kind == 2) g.n_first = (int)a[0].N;
     return launch_g(all, g);
 }
 
