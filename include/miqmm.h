@@ -102,14 +102,16 @@ typedef struct miqmm_problem {
  * Several independent projections that share M, K, group_size, bits and
  * dtypes.  When M <= 2 and every N < 65536 (decode projections) they run as
  * one launch per four problems:
- *  - M == 1, up to four problems sharing x whose codes, scales and biases lie
- *    one after another in memory (a loader that fuses q/k/v or gate/up), on
- *    rows the K-sliced GEMV takes (K >= 2048, or at most 32 16-byte chunks
- *    per row) with 4-byte aligned scales: one K-sliced GEMV over all their
- *    rows, each row stored to its problem's output; every result equals,
- *    bit for bit, the matching rows of miqmm_quantized_matmul_ex with
- *    MIQMM_ROUTE_QMVS on the fused matrix (plus the bias as
- *    miqmm_quantized_linear adds it);
+ *  - M == 1, up to four problems sharing x (the same pointer), on rows the
+ *    K-sliced GEMV takes (K*bits/8 <= 15 KiB, K/group_size even) with 4-byte
+ *    aligned scales and biases: one K-sliced GEMV over all their rows, each
+ *    row stored to its problem's output; every result equals, bit for bit,
+ *    the matching rows of miqmm_quantized_matmul_ex with MIQMM_ROUTE_QMVS on
+ *    the problems' matrices stacked into one (plus the bias as
+ *    miqmm_quantized_linear adds it).  Codes, scales and biases stored one
+ *    after another (a loader that fuses q/k/v or gate/up) are read as that
+ *    one matrix; in separate allocations each block reads one problem's
+ *    rows, which costs one scalar memory round trip per launch more;
  *  - otherwise one v_dot2 GEMV launch per four problems, each result equal,
  *    bit for bit, to miqmm_quantized_matmul_ex with MIQMM_ROUTE_QMV_DOT on it
  *    alone (plus the bias).
