@@ -331,7 +331,8 @@ def cpu_baseline(miqmm, torch, projs, budget_s=15.0):
 
     O.build_c_oracle()
     info = host_info()
-    # the host's CPU share: OMP_NUM_THREADS when set (the GPU box sets it), else every core available
+    # the host's CPU share: OMP_NUM_THREADS when set (a shared host's scheduler sets it), else every core
+    # available
     threads = int(os.environ.get("OMP_NUM_THREADS") or info["affinity"] or info["nproc"] or 1)
     host = []
     for p in projs:
@@ -513,8 +514,9 @@ def main():
                     help="run only this measured section and print its figures (for rocprofv3 summaries)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: the quantized-matmul path has no multi-GPU leg here "
-              "(sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only: the quantized-matmul path has no multi-GPU leg "
+              "(each GPU would run its shard of the projections with these kernels); run with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
