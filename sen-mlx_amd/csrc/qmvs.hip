@@ -505,6 +505,19 @@ int rows_per_block(int64_t N, int ks) {
     return 4;
 }
 
+// rows per block for M rows of x
+int rows_for(int64_t M, int64_t N, int ks) {
+    int rb = rows_per_block(N, ks);
+    if (M > 2 && rb > 8) rb = 8;  // four rows of x: RB * 4 <= 32 sums per wave
+    // two rows of x on rows of one or two slices: 8 rows per block unless 16
+    // still gives 12 waves per CU (measured on MI355X, 4-bit g64: 4096 ->
+    // 14336 9.9-10.4 -> 9.1-9.5 us; with more slices, or more waves, 16 rows
+    // stay faster: 14336 -> 4096 10.0 against 10.2, the 896 -> 151936 head
+    // 18.3-18.8 against 20.9)
+    if (M == 2 && rb == 16 && ks <= 2 && (N + 15) / 16 * ks < 12 * (int64_t)num_cus()) rb = 8;
+    return rb;
+}
+
 // NC: a group in separate allocations; a.N is then all the problems' rows
 // (for the rows per block of their concatenation) and n_first problem 0's
 template <int BITS, int SBT, int RB, int ND, bool YF32, bool BIAS, bool HALF, int MX, bool NC>
@@ -555,9 +568,7 @@ hipError_t launch_nd(const QmmArgs& a, const QmvsGroup& g, int ks) {
 template <int BITS, int SBT, bool YF32, bool BIAS, int MX>
 hipError_t launch_rb(const QmmArgs& a, const QmvsGroup& g) {
     const int ks = slices(a.K, BITS);
-    int rb = rows_per_block(a.N, ks);
-    if (MX == 4 && rb > 8) rb = 8;  // RB * MX <= 32 sums per wave
-    switch (rb) {
+    switch (rows_for(a.M, a.N, ks)) {
 #if QMVS_RB_FORCE == 32
         case 32: return launch_nd<BITS, SBT, 32, YF32, BIAS, 1>(a, g, ks);
 #endif
@@ -606,7 +617,7 @@ bool qmvs_supported(int64_t M, int64_t N, int64_t K, int bits, int group_size) {
 }
 
 void qmvs_config(const QmmArgs& a, int* rows_per_blk, int* slices_out, int* blocks) {
-    const int ks = slices(a.K, a.bits), rb = rows_per_block(a.N, ks);
+    const int ks = slices(a.K, a.bits), rb = rows_for(a.M, a.N, ks);
     if (rows_per_blk) *rows_per_blk = rb;
     if (slices_out) *slices_out = ks;
     if (blocks) *blocks = (int)((a.N + rb - 1) / rb);
