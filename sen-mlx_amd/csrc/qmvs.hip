@@ -1,16 +1,20 @@
-// qmvs.hip -- K-sliced GEMV for one row of x (M = 1) over long rows.
+// qmvs.hip -- K-sliced GEMV for one to four rows of x (M <= 4).
 //
-//   y[n] = sum_k x[k] * (s[n, k/g] * q[n, k] + b[n, k/g])             (transpose=true)
+//   y[m, n] = sum_k x[m, k] * (s[n, k/g] * q[n, k] + b[n, k/g])       (transpose=true)
 //
-// The decode-time call of every large quantized projection of the reference
-// (src/engine/mlx_lm/models/llama.rs:195-197,249,293-294 with x [1, 1, K]).
+// The decode-time call of every quantized projection of the reference
+// (src/engine/mlx_lm/models/llama.rs:195-197,249,293-294 with x [1, 1, K]),
+// and the few-row calls of several sequences or speculative tokens; also the
+// decode step's grouped q/k/v and gate/up (QmvsGroup).
 //
 // HBM-bound design (no MFMA).  A row of W is cut into K-slices of 1 KiB of
 // codes (2048 4-bit or 1024 8-bit codes).  A block covers RB consecutive rows
 // with one wave per K-slice; lane l of wave w owns the 16-byte chunk l of
 // slice w in each of the block's rows.  A wave runs straight through, with
 // no loop:
-//   - it loads its x chunk (the same for every row it computes), then issues
+//   - it loads its x chunk of every row of x (the same for every row of W it
+//     computes; with several rows of x each row of codes is unpacked once and
+//     dotted with all of them), then issues
 //     the scales and biases of its RB rows (one 1 KiB run per row stride,
 //     copied straight to the wave's LDS by direct-to-LDS loads) and the
 //     codes of its RB rows (each load instruction 1 KiB contiguous bytes of
@@ -36,9 +40,10 @@
 // value against bf16 x.  The offsets and scales are undone per row in fp32:
 //   sum_k x_k q_k = dot - 128 * sum x, or 2^E (dot - 1024 * sum of the x operands).
 // Measured on MI355X (cold weights, back-to-back graph launches, 4-bit g64):
-// M = 1, 4096 -> 14336 and 14336 -> 4096 in 7.9 us (4.2 TB/s) against 9.2 and
-// 9.9 us for the v_dot2 GEMV; the 5376 -> 262144 head in 113 us (7.0 TB/s);
-// a bare streaming read of the same 33 MB takes 5.9 us.
+// M = 1, 4096 -> 14336 and 14336 -> 4096 in 7.9-8.4 us (about 4 TB/s) against
+// 9.2 and 9.9 us for the v_dot2 GEMV, beside 5.9-6.2 us for a bare streaming
+// read of the same 33 MB; the 5376 -> 262144 head (g32, fp16 scales) in
+// 113-131 us (6.7-7.8 TB/s); M = 2 and 4 on 4096 -> 14336 in 8.9 and 11.8 us.
 #include <climits>
 #include <type_traits>
 
