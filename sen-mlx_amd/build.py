@@ -67,7 +67,48 @@ def build(jobs: int = 4) -> str:
     return LIB
 
 
+def _usage(src: str) -> dict:
+    """Register use of every kernel instantiation of one source (device pass only)."""
+    os.makedirs(BUILD, exist_ok=True)
+    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".usage.o")
+    cmd = [hipcc(), *FLAGS, *FILE_FLAGS.get(src, []), "--offload-device-only",
+           "-Rpass-analysis=kernel-resource-usage", "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stderr}")
+    os.remove(obj)
+    out = {"kernels": 0, "vgpr_spill": 0, "scratch": 0, "sgpr_spill": 0}
+    for line in r.stderr.splitlines():
+        if "Function Name:" in line:
+            out["kernels"] += 1
+        for key, tag in (("vgpr_spill", "VGPRs Spill:"), ("sgpr_spill", "SGPRs Spill:"),
+                         ("scratch", "ScratchSize [bytes/lane]:")):
+            if tag in line and int(line.split(tag)[1].split()[0]) > 0:
+                out[key] += 1
+    return out
+
+
+def resource_usage(jobs: int = 4) -> bool:
+    """Prints, per HIP source, how many kernel instantiations spill VGPRs, use
+    scratch memory or spill SGPRs (SGPR spills go to VGPR lanes, not memory);
+    False if any instantiation spills VGPRs or uses scratch."""
+    srcs = [s for s in SOURCES if s.endswith(".hip")]
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        res = list(ex.map(_usage, srcs))
+    ok = True
+    for src, u in zip(srcs, res):
+        print(f"{src}: {u['kernels']} kernels, VGPR spills {u['vgpr_spill']}, scratch {u['scratch']}, "
+              f"SGPR spills (to VGPR lanes) {u['sgpr_spill']}")
+        ok = ok and u["vgpr_spill"] == 0 and u["scratch"] == 0
+    return ok
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
-    print(build(ap.parse_args().jobs))
+    ap.add_argument("--resource-usage", action="store_true",
+                    help="report spills and scratch of every kernel instantiation instead of building")
+    args = ap.parse_args()
+    if args.resource_usage:
+        sys.exit(0 if resource_usage(args.jobs) else 1)
+    print(build(args.jobs))
