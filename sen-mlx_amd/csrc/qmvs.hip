@@ -69,6 +69,7 @@ constexpr int kSliceBytes = 1024;  // codes per K-slice: 64 lanes x 16 bytes
 template <int BITS, int RB, bool HALF, int MX>
 constexpr bool f16_operands() { return BITS == 4 && MX == 1 && RB == 16 && !HALF; }
 typedef __attribute__((ext_vector_type(2))) _Float16 half2_t;
+typedef __attribute__((ext_vector_type(2))) unsigned short u16x2_t;
 
 
 struct QmvsArgs {
@@ -351,24 +352,32 @@ __global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uin
         // 1/16; xsc = 2^E and xoff = -2^E * 1024 * (sum of the operands) undo
         // the scale and the codes' 1024 offset
         if constexpr (F16) {
-            uint32_t emax = 0;
+            // the largest exponent field: a packed 16-bit max of the pairs'
+            // exponent bits
+            uint32_t em = 0;
 #pragma unroll
-            for (int i = 0; i < NP; ++i) emax = max(emax, max((xw[m][i] >> 7) & 0xFFu, (xw[m][i] >> 23) & 0xFFu));
-            const int e = (int)emax - 127;
+            for (int i = 0; i < NP; ++i)
+                em = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, xw[m][i] & 0x7F807F80u),
+                                                                            __builtin_bit_cast(u16x2_t, em)));
+            const int e = (int)(max(em & 0xFFFFu, em >> 16) >> 7) - 127;
             xsc[m] = __builtin_amdgcn_ldexpf(1.f, e);
-            auto h = [&](int k, int extra) {  // x_k of the chunk, scaled, as fp16 bits
+            // x_k of the chunk times 2^-e (or 2^-e-4) as fp16 bits: the product
+            // is exact in fp32, so the multiply and the conversion fuse into one
+            // v_fma_mixlo_f16 with the bits of ldexp then convert
+            const float sc0 = __builtin_amdgcn_ldexpf(1.f, -e), sc4 = __builtin_amdgcn_ldexpf(1.f, -e - 4);
+            auto h = [&](int k, float sc) {
                 const uint32_t w = xw[m][k >> 1];
                 const float f = __uint_as_float((k & 1) ? (w & 0xFFFF0000u) : (w << 16));
-                return (uint32_t)f32_to_f16_bits(__builtin_amdgcn_ldexpf(f, -e - extra));
+                return (uint32_t)f32_to_f16_bits(f * sc);
             };
             float ssum = 0.f;
 #pragma unroll
             for (int wi = 0; wi < 4; ++wi) {
                 const int k0 = 8 * wi;
-                X[m][4 * wi + 0] = h(k0 + 0, 0) | (h(k0 + 4, 0) << 16);
-                X[m][4 * wi + 1] = h(k0 + 1, 4) | (h(k0 + 5, 4) << 16);
-                X[m][4 * wi + 2] = h(k0 + 2, 0) | (h(k0 + 6, 0) << 16);
-                X[m][4 * wi + 3] = h(k0 + 3, 4) | (h(k0 + 7, 4) << 16);
+                X[m][4 * wi + 0] = h(k0 + 0, sc0) | (h(k0 + 4, sc0) << 16);
+                X[m][4 * wi + 1] = h(k0 + 1, sc4) | (h(k0 + 5, sc4) << 16);
+                X[m][4 * wi + 2] = h(k0 + 2, sc0) | (h(k0 + 6, sc0) << 16);
+                X[m][4 * wi + 3] = h(k0 + 3, sc4) | (h(k0 + 7, sc4) << 16);
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
                     ssum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, X[m][4 * wi + t]),
@@ -396,8 +405,10 @@ __global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uin
     // this lane's scale / bias of row j at j * sb + 2 * (group in slice)
     const uint32_t sl_off = (uint32_t)((lc << CPC_SHIFT) >> gs_shift) * 2;
     // per-lane partial of every row; in the wave of the slice that runs past
-    // the row end (if any), lanes past it take zero scales and biases, so
-    // they add nothing whatever their LDS holds
+    // the row end (if any), lanes past it add nothing whatever their LDS
+    // holds: with one row of x their partials are zeroed (one select per
+    // row), with more their scales and biases (two per row, not one per row
+    // of x); their x reads zero
     const bool partial = __builtin_amdgcn_readfirstlane((int)(ws == KS - 1 && (C & 63) != 0)) != 0;
     float part[RL * MX];  // value m * RL + j
     auto rows = [&](auto masked) {
@@ -407,7 +418,7 @@ __global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uin
             const int jr = rh + j;  // row of the block
             float s = half_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(wl + jr * sb + sl_off));
             float b = half_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(wl + ND * kSliceBytes + jr * sb + sl_off));
-            if constexpr (decltype(masked)::value) {
+            if constexpr (decltype(masked)::value && MX > 1) {
                 s = cv ? s : 0.f;
                 b = cv ? b : 0.f;
             }
@@ -429,6 +440,7 @@ __global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uin
                         a = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, X[m][i]),
                                                    __builtin_bit_cast(half2_t, p[i]), a, false);
                     part[m * RL + j] = fmaf(s, fmaf(a, xsc[m], xoff[m]), b * xs[m]);
+                    if constexpr (decltype(masked)::value && MX == 1) part[m * RL + j] = cv ? part[m * RL + j] : 0.f;
                 }
                 continue;
             }
@@ -444,6 +456,7 @@ __global__ __launch_bounds__((max_threads<RB, MX>())) void qmvs_kernel(const uin
 #pragma unroll
                 for (int i = 0; i < NP; ++i) a = dot2(X[m][i], p[i], a);
                 part[m * RL + j] = fmaf(b, xs[m], s * a);
+                if constexpr (decltype(masked)::value && MX == 1) part[m * RL + j] = cv ? part[m * RL + j] : 0.f;
             }
         }
     };
