@@ -59,7 +59,7 @@ constexpr int kSliceBytes = 1024;  // codes per K-slice: 64 lanes x 16 bytes
 // Operands of the 4-bit dot products: fp16 (codes at bits 0-3 and 4-7 of each
 // half are exact fp16 mantissas: per word of eight codes one shift and four
 // and-ors, against three shifts and four for bf16) costs x a preparation of
-// ~180 VALU instructions per lane (its largest exponent, a power-of-two scale
+// ~150 VALU instructions per lane (its largest exponent, a power-of-two scale
 // and the conversions) against ~30 for bf16 (a re-pairing), so it pays only
 // where a lane has many rows to amortise it: one row of x and 16 full rows per
 // lane (measured on MI355X, 4-bit g64: 14336 -> 4096 8.39 -> 8.13 us with fp16;
