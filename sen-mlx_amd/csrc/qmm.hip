@@ -626,9 +626,12 @@ __global__ __launch_bounds__(1024) void gather_plan_kernel(const int32_t* idx, i
 // 0.0202 us per unit of K, a 256-wide one (eight waves) 1.3x that; a split
 // into ks k ranges divides the tile time by ks and adds the partial traffic
 // (ks fp32 values per output written, then read back by the reduce kernel,
-// at a measured 1.6 TB/s effective) and the reduce kernel's launch.  E.g. M = 2048: N = 14336 and 6144 -> 256 wide, N = 4096 ->
-// 128 wide at K = 4096 and 256 wide in two k ranges at K = 14336; M = 256,
-// N = 4096, K = 4096 -> 128 wide in four k ranges.
+// at 2.4 TB/s effective: fitted to forced plans on MI355X, 2.2-3.1 TB/s at
+// M = 256-1024) and the reduce kernel's launch.  E.g. M = 2048: N = 14336
+// and 6144 -> 256 wide, N = 4096 -> 128 wide at K = 4096 and 256 wide in two
+// k ranges at K = 14336; M = 1024, N = K = 4096 -> 128 wide in two k ranges
+// (60.8 us against 67.2 unsplit); M = 256, N = 4096, K = 4096 -> 128 wide in
+// four k ranges.
 struct QmmPlan {
     int bn, ks;
 };
@@ -644,7 +647,7 @@ QmmPlan plan_qmm(int64_t M, int64_t N, int64_t K, int max_ks) {
             if (ks > 1 && (KT < 8 * ks || (double)ks * M * N * 4 >= 2147483648.0)) break;  // >= 8 k-steps per range
             const double rounds = (double)((tiles * ks + cus - 1) / cus);
             double us = rounds * (bn == 256 ? 1.3 : 1.0) * 0.0202 * (double)K / ks;
-            if (ks > 1) us += (double)M * N * 4 * (2 * ks) / 1.6e6 + 2.0;
+            if (ks > 1) us += (double)M * N * 4 * (2 * ks) / 2.4e6 + 2.0;
             if (us < best_us) {
                 best_us = us;
                 best = {bn, ks};
