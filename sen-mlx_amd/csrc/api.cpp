@@ -120,7 +120,20 @@ int check_launch(hipError_t e, const char* what) {
 //          where the group-diagonal MFMA GEMV is faster; rows the LDS-staged
 //          GEMV does not take go to the group-diagonal one too;
 //   5 <= M <= 16: the group-diagonal MFMA GEMV, whose cost barely grows with M;
+//   17 <= M <= 32 (64 for rows of K >= 8192): the GEMVs in passes of 16 rows
+//          of x (the last pass routed by its own rows), against 256-row tiles
+//          of the tiled matmul that are mostly empty: M = 17 / 32, 4096 ->
+//          14336 33.3 / 34.9 -> 23.7 / 30.5 us, 14336 -> 4096 63.3 / 64.0 ->
+//          22.1 / 28.3, 4096 -> 4096 24.0 / 24.3 -> 13.5 / 18.2; at M = 48
+//          three passes lose to the tiled matmul at K = 4096 (about 45
+//          against 36.4 and 27.6 against 24.5 us) and win on 14336 -> 4096
+//          (about 43 against 64.0);
 //   larger M: the tiled MFMA matmul.
+constexpr int64_t kGemvRows = 16;  // rows of x per pass of the GEMVs
+
+// the largest M the auto route gives the GEMVs (in passes of 16 rows)
+int64_t gemv_max_m(int64_t K) { return K >= 8192 ? 64 : 32; }
+
 int auto_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, bool sb_aligned4 = true) {
     if (M <= 4 && sb_aligned4 && miqmm::qmvs_supported(M, N, K, bits, group_size)) return MIQMM_ROUTE_QMVS;
     if (M == 1) {
@@ -129,7 +142,7 @@ int auto_route(int64_t M, int64_t N, int64_t K, int group_size, int bits, bool s
     }
     if (M <= 4 && miqmm::qmvx_supported(M, K, group_size) && !(M >= 3 && N >= 8192)) return MIQMM_ROUTE_QMVX;
     if (M <= 4 && (K / group_size) % 2 != 0) return MIQMM_ROUTE_QMV_DOT;
-    return M <= 16 ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
+    return M <= gemv_max_m(K) ? MIQMM_ROUTE_QMV : MIQMM_ROUTE_QMM;
 }
 
 // argument checks shared by the single and grouped entry points; MIQMM_OK
@@ -184,11 +197,16 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
 
     miqmm::QmmArgs a{y, x, w, scales, biases, bias, M, N, K, group_size, bits, x_dtype, sb_dtype, y_dtype,
                      reinterpret_cast<hipStream_t>(stream)};
-    if (route == MIQMM_ROUTE_AUTO) route = auto_route(M, N, K, group_size, bits, aligned4(scales) && aligned4(biases));
+    const bool sb4 = aligned4(scales) && aligned4(biases);
+    const bool automatic = route == MIQMM_ROUTE_AUTO;
+    if (automatic) route = auto_route(M, N, K, group_size, bits, sb4);
     if (route == MIQMM_ROUTE_QMVS) return check_launch(miqmm::launch_qmvs(a), "qmvs launch");
     if (route == MIQMM_ROUTE_QMV || route == MIQMM_ROUTE_QMV_DOT || route == MIQMM_ROUTE_QMVX) {
-        // the GEMV kernels handle at most 16 (qmvx: 4) rows of x per pass over W
-        const int64_t step = route == MIQMM_ROUTE_QMVX ? 4 : 16;
+        // the GEMV kernels handle at most 16 (qmvx: 4) rows of x per pass over
+        // W; passes run in order on the stream, so the split GEMV's partials
+        // reuse one workspace; with the route chosen here each pass takes the
+        // route of its own rows (the last pass at M > 16 may be a few rows)
+        const int64_t step = route == MIQMM_ROUTE_QMVX ? 4 : kGemvRows;
         for (int64_t m0 = 0; m0 < M; m0 += step) {
             miqmm::QmmArgs part = a;
             const int64_t mm = M - m0 < step ? M - m0 : step;
@@ -196,11 +214,13 @@ int qmm_common(void* y, const void* x, const uint32_t* w, const void* scales, co
             part.x = static_cast<const uint16_t*>(x) + m0 * K;
             const int ysz = y_dtype == MIQMM_DT_F32 ? 4 : 2;
             part.y = static_cast<char*>(y) + m0 * N * ysz;
-            st = route == MIQMM_ROUTE_QMV    ? check_launch(miqmm::launch_qmv_mfma_split(part, workspace,
-                                                                                         workspace_bytes),
-                                                            "qmv launch")
-                 : route == MIQMM_ROUTE_QMVX ? check_launch(miqmm::launch_qmvx(part), "qmvx launch")
-                                             : check_launch(miqmm::launch_qmv(part), "qmv_dot launch");
+            const int r = automatic && mm < M ? auto_route(mm, N, K, group_size, bits, sb4) : route;
+            st = r == MIQMM_ROUTE_QMV    ? check_launch(miqmm::launch_qmv_mfma_split(part, workspace,
+                                                                                     workspace_bytes),
+                                                        "qmv launch")
+                 : r == MIQMM_ROUTE_QMVS ? check_launch(miqmm::launch_qmvs(part), "qmvs launch")
+                 : r == MIQMM_ROUTE_QMVX ? check_launch(miqmm::launch_qmvx(part), "qmvx launch")
+                                         : check_launch(miqmm::launch_qmv(part), "qmv_dot launch");
             if (st != MIQMM_OK) return st;
         }
         return ok();
@@ -218,7 +238,16 @@ int64_t split_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size, i
     a.K = K;
     a.group_size = group_size;
     a.bits = bits;
-    return route == MIQMM_ROUTE_QMM ? miqmm::qmm_workspace_bytes(a) : miqmm::qmv_split_bytes(a);
+    if (route == MIQMM_ROUTE_QMM) return miqmm::qmm_workspace_bytes(a);
+    // passes of 16 rows (one workspace, reused in order): the largest need
+    int64_t need = 0;
+    for (int64_t m0 = 0; m0 < M; m0 += kGemvRows) {
+        a.M = M - m0 < kGemvRows ? M - m0 : kGemvRows;
+        if (a.M < M && auto_route(a.M, N, K, group_size, bits) != MIQMM_ROUTE_QMV) continue;
+        const int64_t n = miqmm::qmv_split_bytes(a);
+        need = n > need ? n : need;
+    }
+    return need;
 }
 
 
@@ -520,7 +549,10 @@ int miqmm_query_route(int64_t M, int64_t N, int64_t K, int group_size, int bits,
     if (route_out) *route_out = route;
     if (tile_out) {
         tile_out[0] = tile_out[1] = tile_out[2] = tile_out[3] = 0;
-        if (route == MIQMM_ROUTE_QMV) miqmm::qmv_mfma_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
+        if (route == MIQMM_ROUTE_QMV) {  // the first pass's launch (16 rows of x at M > 16)
+            a.M = M < kGemvRows ? M : kGemvRows;
+            miqmm::qmv_mfma_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
+        }
         else if (route == MIQMM_ROUTE_QMVX) miqmm::qmvx_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
         else if (route == MIQMM_ROUTE_QMV_DOT) miqmm::qmv_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);
         else if (route == MIQMM_ROUTE_QMVS) miqmm::qmvs_config(a, &tile_out[0], &tile_out[1], &tile_out[2]);

@@ -242,12 +242,23 @@ def test_query_route(lib):
     for M in (5, 8, 16):
         route, tiles = miqmm.query_route(M, 14336, 4096, 64, 4)
         assert route == miqmm.ROUTE_QMV and tiles[0] in (1, 2, 4) and tiles[1] >= M and tiles[2] in (4, 16)
+    # M = 17..32: the GEMVs in two passes (the launch of the first, 16 rows, reported)
+    for M in (17, 24, 32):
+        route, tiles = miqmm.query_route(M, 14336, 4096, 64, 4)
+        assert route == miqmm.ROUTE_QMV and tiles[1] == 16, (M, tiles)
+    assert miqmm.query_route(33, 14336, 4096, 64, 4)[0] == miqmm.ROUTE_QMM
+    # rows of K >= 8192: passes up to M = 64
+    assert miqmm.query_route(64, 4096, 14336, 64, 4)[0] == miqmm.ROUTE_QMV
+    assert miqmm.query_route(65, 4096, 14336, 64, 4)[0] == miqmm.ROUTE_QMM
+    # the workspace of two passes: the larger pass's partials, reused in order
+    assert miqmm.workspace_size(32, 4096, 14336) == miqmm.workspace_size(16, 4096, 14336) > 0
+    assert miqmm.workspace_size(17, 4096, 14336) == miqmm.workspace_size(16, 4096, 14336)
     route, tiles = miqmm.query_route(2048, 14336, 4096, 64, 4)
     assert route == miqmm.ROUTE_QMM and tiles[2] == 64
     # the qmm plan (rounds of one tile per CU): width and k ranges
     for (M, N, K), (bn, ks) in {(2048, 14336, 4096): (256, 1), (2048, 6144, 4096): (256, 1),
                                 (2048, 4096, 4096): (128, 1), (2048, 4096, 14336): (256, 2),
-                                (256, 4096, 4096): (128, 4), (32, 64, 256): (128, 1)}.items():
+                                (256, 4096, 4096): (128, 4), (33, 64, 256): (128, 1)}.items():
         route, tiles = miqmm.query_route(M, N, K, 64, 4)
         assert route == miqmm.ROUTE_QMM and tiles == (256, bn, 64, ks), ((M, N, K), tiles)
     # the MFMA GEMV's launch shape (unsplit): four tiles per block where that
