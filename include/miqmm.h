@@ -72,11 +72,13 @@ typedef enum {
  * (reached at src/engine/mlx_lm/utils/mod.rs:70-78 and from every
  * QuantizedLinear::forward).  transpose must be 1; bits in {4, 8};
  * group_size in {32, 64, 128}; K % group_size == 0; x and w 16-byte aligned.
- * M == 0 is a no-op.  Route (HBM-bound GEMVs for M <= 16): M <= 4 -> qmvs
+ * M == 0 is a no-op.  Route (HBM-bound GEMVs for M <= 32): M <= 4 -> qmvs
  * wherever it takes the shape (K*bits/8 <= 15 KiB, 8 KiB with M > 2;
  * K/group_size even; 4-byte aligned scales and biases); else M == 1 ->
  * qmv_dot, or qmvx for N >= 65536 with K <= 2048; 2 <= M <= 4 -> qmvx where
  * supported, else qmv (or qmv_dot with an odd K/group_size); M <= 16 -> qmv;
+ * M <= 32 (64 with K >= 8192) -> the GEMVs in passes of 16 rows of x, the
+ * last pass routed by its own rows;
  * else qmm (MFMA-bound tiled matmul).
  */
 int miqmm_quantized_matmul(void* y, const void* x, const uint32_t* w, const void* scales,
@@ -140,9 +142,9 @@ int miqmm_quantized_matmul_ex(void* y, const void* x, const uint32_t* w, const v
 /*
  * Bytes of scratch that miqmm_quantized_matmul_ws would use for this shape
  * (fp32 partials of a k split: k ranges * M * N * 4, else 0).  The tiled
- * matmul (M > 16) splits its k-steps over several blocks per output tile
+ * matmul (larger M) splits its k-steps over several blocks per output tile
  * when the output tiles are fewer than the CUs; the small-M MFMA GEMV
- * (5 <= M <= 16) splits K over blocks of 128 rows, each reading its range
+ * (5 <= M <= 16 rows per pass) splits K over blocks of 128 rows, each reading its range
  * of x once, for rows of K >= 8192 codes and, at M > 8, outputs of
  * N >= 8192.
  * No reference counterpart: the workspace query of the caller that can
